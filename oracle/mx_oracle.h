@@ -1,0 +1,115 @@
+/*
+ * mx_oracle.h -- CPU oracle for the MXFP8 flash-attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference's
+ * MX quantization rules and of its streaming (online-softmax) MX attention
+ * recurrence.  It is linked only by tests/, by __graft_entry__.smoke() and by
+ * bench.py's cpu_baseline leg, always as the checker.  The product library
+ * (libmxfa) never calls it.
+ *
+ * Reference semantics restated here (paths relative to the reference tree):
+ *   - element/scale rules ("R1"): lib/golden/mx_fp_math.h:11-28 (bf16 RNE),
+ *     :205-225 (E4M3 encode), :227-236 (E4M3 decode), :249-252 (E8M0),
+ *     :256-264 (E3M2 decode), :266-335 (bf16 -> E3M2 code pipeline);
+ *     lib/golden/mx_golden.cpp:146-190 (block-32 requant post-pass:
+ *     scale = floor(log2f(amax)) - {8 | 4} + 127, clamp [0,254], amax==0 -> 0).
+ *   - attention recurrence: kernels/flash_attention_mx_gemma/
+ *     flash_attention_model.py:317-372 (scale -> softcap -> mask -> block max ->
+ *     corr -> exp -> requant P -> PV -> rescale; deferred 1/l with l<=0 -> 0),
+ *     kernels/flash_attention_mx_gqa/flash_attention_model.py:175-248 (GQA
+ *     head sharing h -> h / (Hq/Hkv), causal key_pos > query_pos masking,
+ *     q_pos0), kernels/flash_attention_mx_gqa/fa_gen_data.py:95-117 (Q, K
+ *     blocked along D; V blocked along the key axis).
+ *
+ * Deliberate, documented differences from the reference's bf16 Python model
+ * (whose fp8_matmul_model dependency is not vendored): arithmetic is done in
+ * double and P is rounded to fp32 before requantization, because the
+ * MI355X kernels compute in fp32; the P requant rule is R1 (lib/golden),
+ * which is the rule the build targets.
+ */
+#ifndef MX_ORACLE_H
+#define MX_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_FMT_E4M3 0
+#define ORC_FMT_E3M2 1
+
+/* floorf(log2f(x)) for finite x > 0, bit-exact with the glibc libm that the
+ * reference's lib/golden code calls (mx_fp_math.h:209, mx_golden.cpp:171).
+ * Computed from the exponent plus a per-binade mantissa threshold table that
+ * orc_init() derives by correctly rounding log2 to float. */
+int      orc_floor_log2f(float x);
+/* The derived tables, for tests: thr[E] (E = biased exponent 1..254) is the
+ * smallest 23-bit mantissa at which floorf(log2f) returns e+1 (0x800000 =
+ * never); sub_thr[p] is the same for subnormals whose leading bit is p. */
+void     orc_log2_tables(uint32_t thr[256], uint32_t sub_thr[23]);
+
+uint16_t orc_f32_to_bf16(float x);           /* mx_fp_math.h:11-28 */
+float    orc_bf16_to_f32(uint16_t b);
+uint8_t  orc_e4m3_encode(float v);           /* mx_fp_math.h:205-225 */
+float    orc_e4m3_decode(uint8_t c);         /* mx_fp_math.h:227-236 */
+uint8_t  orc_e3m2_encode_bf16(uint16_t b);   /* mx_fp_math.h:266-335 */
+float    orc_e3m2_decode(uint8_t c);         /* mx_fp_math.h:256-264 */
+double   orc_e8m0_decode(uint8_t c);         /* mx_fp_math.h:249-252 (NaN for 255) */
+uint8_t  orc_scale_code(float amax, int fmt);/* mx_golden.cpp:169-174 */
+
+/* Quantize n values (stride apart) as one MX block (n <= 32): writes codes
+ * (code_stride apart) and returns the E8M0 scale code. mx_golden.cpp:162-190. */
+uint8_t  orc_quantize_block(const float *v, int64_t stride, int n, int fmt,
+                            uint8_t *codes, int64_t code_stride);
+/* Row-blocked: scales[rows][cols/32].  Column-blocked: scales[rows/32][cols]. */
+void     orc_quantize_rows(const float *x, int64_t rows, int64_t cols, int fmt,
+                           uint8_t *codes, uint8_t *scales);
+void     orc_quantize_cols(const float *x, int64_t rows, int64_t cols, int fmt,
+                           uint8_t *codes, uint8_t *scales);
+double   orc_decode_elem(uint8_t code, int fmt);
+
+typedef struct {
+  int32_t batch, num_q_heads, num_kv_heads, seq_q, seq_k, head_dim;
+  int32_t causal;       /* key visible only if kpos <= qpos                         */
+  int32_t q_pos0;       /* global position of query row 0                           */
+  int32_t window;       /* 0 = off; else key also masked if kpos + window <= qpos   */
+  float   softmax_scale;
+  float   softcap;      /* 0 = off; else s <- cap*tanh(s/cap) after the scale      */
+  int32_t v_fmt;        /* ORC_FMT_E4M3 / ORC_FMT_E3M2 (Q, K are always E4M3)      */
+} orc_attn_params;
+
+/* Streaming MX attention over key blocks of block_n keys (block j covers keys
+ * [j*block_n, (j+1)*block_n)).  split_len > 0 splits the keys into independent
+ * chunks of split_len keys that are merged by log-sum-exp (the split-KV decode
+ * schedule); 0 = one pass.  heads: optional list of nheads flattened (b*Hq+h)
+ * indices to compute (others untouched); NULL = all.  Layouts:
+ *   q [B][Hq][Sq][D], q_sc [B][Hq][Sq][D/32]
+ *   k [B][Hkv][Sk][D], k_sc [B][Hkv][Sk][D/32]
+ *   v [B][Hkv][Sk][D], v_sc [B][Hkv][Sk/32][D]
+ *   o [B][Hq][Sq][D] fp32
+ * Returns 0 on success, -1 on invalid arguments. */
+int orc_attention(const orc_attn_params *p,
+                  const uint8_t *q, const uint8_t *q_sc,
+                  const uint8_t *k, const uint8_t *k_sc,
+                  const uint8_t *v, const uint8_t *v_sc,
+                  float *o, int block_n, int split_len,
+                  const int32_t *heads, int nheads, int nthreads);
+
+/* Unquantized fp64 softmax attention on the dequantized operands (no P
+ * requant, no streaming): the sanity reference. Same layouts/params. */
+int orc_attention_dense(const orc_attn_params *p,
+                        const uint8_t *q, const uint8_t *q_sc,
+                        const uint8_t *k, const uint8_t *k_sc,
+                        const uint8_t *v, const uint8_t *v_sc,
+                        float *o, const int32_t *heads, int nheads, int nthreads);
+
+/* Self-checks used by the tests. */
+int64_t orc_check_log2_vs_libm(uint32_t lo, uint32_t hi);
+void    orc_e4m3_encode_range(uint32_t bits_lo, uint32_t count, uint8_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,180 @@
+"""CPU tests pinning the oracle's MX element and scale rules.
+
+Pins, in order of strength:
+  * committed fixtures written from the reference's own lib/golden code
+    (tests/golden/make_golden.py): decode tables, the E3M2 encoder over all
+    65536 bf16 patterns, the E4M3 encoder on edge cases, and the mx_golden
+    CLI's block-32 requant post-pass (codes + E8M0 scales);
+  * the reference's compiled code itself (oracle/_ref) where it was built;
+  * closed forms: the OCP E4M3/E3M2 grids, libm's floorf(log2f(x)) over every
+    positive float, and scale-range invariants.
+"""
+import ctypes
+import os
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_decode_tables_match_reference_fixture():
+    z = np.load(os.path.join(GOLD, "decode_tables.npz"))
+    L = O.lib()
+    e4 = np.array([L.orc_e4m3_decode(c) for c in range(256)], np.float32)
+    e3 = np.array([L.orc_e3m2_decode(c) for c in range(64)], np.float32)
+    e8 = np.array([L.orc_e8m0_decode(c) for c in range(255)], np.float64)
+    np.testing.assert_array_equal(e4, z["e4m3"])
+    np.testing.assert_array_equal(e3, z["e3m2"])
+    np.testing.assert_array_equal(e8.astype(np.float32), z["e8m0"])
+    assert np.isnan(L.orc_e8m0_decode(255))
+
+
+def test_decode_closed_forms():
+    """OCP E4M3: bias 7, subnormal step 2^-9, max 448; E3M2: bias 3, step 2^-4, max 28."""
+    L = O.lib()
+    assert L.orc_e4m3_decode(0x7E) == 448.0 and L.orc_e4m3_decode(0x08) == 2.0 ** -6
+    assert L.orc_e4m3_decode(0x01) == 2.0 ** -9 and L.orc_e4m3_decode(0x38) == 1.0
+    assert L.orc_e3m2_decode(0x1F) == 28.0 and L.orc_e3m2_decode(0x01) == 0.0625
+    assert L.orc_e3m2_decode(0x0C) == 1.0 and L.orc_e3m2_decode(0x3F) == -28.0
+
+
+def test_e3m2_encoder_all_bf16_vs_fixture():
+    want = np.fromfile(os.path.join(GOLD, "e3m2_encode.bin"), np.uint8)
+    L = O.lib()
+    got = np.array([L.orc_e3m2_encode_bf16(b) for b in range(65536)], np.uint8)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_e3m2_encoder_is_nearest_on_grid():
+    """Independent check: in the scaled range the E3M2 code is the nearest E3M2 value
+    of the bf16 input (ties to even mantissa), up to the pipeline's E4M2 double rounding."""
+    L = O.lib()
+    grid = np.array([L.orc_e3m2_decode(c) for c in range(32)], np.float64)
+    rng = np.random.default_rng(1)
+    for v in rng.uniform(0.3, 27.0, 2000).astype(np.float32):
+        b = L.orc_f32_to_bf16(float(v))
+        x = float(np.uint32(b << 16).view(np.float32))
+        code = L.orc_e3m2_encode_bf16(b)
+        err = abs(grid[code] - x)
+        assert err <= np.min(np.abs(grid - x)) + 1e-12 or abs(err - np.min(np.abs(grid - x))) < x * 2 ** -3
+
+
+def test_e4m3_encoder_edge_fixture():
+    z = np.load(os.path.join(GOLD, "e4m3_encode.npz"))
+    L = O.lib()
+    x = z["x"]
+    got = np.array([L.orc_e4m3_encode(float(v)) for v in x], np.uint8)
+    bad = np.nonzero(got != z["code"])[0]
+    assert len(bad) == 0, [(float(x[i]), hex(got[i]), hex(z["code"][i])) for i in bad[:10]]
+
+
+def test_e4m3_encoder_closed_form_on_grid():
+    """Every finite E4M3 value in [2^-6, 448] encodes to its own code (exact grid points)."""
+    L = O.lib()
+    for c in range(256):
+        e = (c >> 3) & 15
+        if e == 0 or (c & 0x7F) == 0x7F:
+            continue
+        assert L.orc_e4m3_encode(L.orc_e4m3_decode(c)) == c
+
+
+def test_floor_log2f_exhaustive_vs_libm():
+    """Every positive finite float: table-based floor(log2) == libm floorf(log2f(x))."""
+    L = O.lib()
+    N, nt = 0x7F800000, 32
+    step = N // nt + 1
+    with ThreadPoolExecutor(min(8, os.cpu_count() or 1)) as ex:
+        bad = sum(ex.map(lambda i: L.orc_check_log2_vs_libm(1 + i * step, min(N, 1 + (i + 1) * step)), range(nt)))
+    assert bad == 0
+
+
+def test_log2_table_shape():
+    """Thresholds sit just below powers of two and are monotone in |e|."""
+    thr, sub = O.log2_tables()
+    for E in range(1, 255):
+        assert thr[E] == 0x800000 or thr[E] >= 0x7FFF00
+    assert thr[127] == 0x800000 and thr[126] == 0x800000    # e = 0, -1: log2 near 1 and 0 is exact enough
+    assert thr[127 + 4] == 0x7FFFFE and thr[127 + 64] == 0x7FFFD4
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference lib/golden not built here")
+def test_e4m3_encoder_vs_reference_whole_range():
+    """Every float in [2^-10, 2^10) of both signs vs the reference's compiled fp8_e4m3_to_code."""
+    L, R = O.lib(), O.ref()
+    lo, hi = int(np.float32(2.0 ** -10).view(np.uint32)), int(np.float32(2.0 ** 10).view(np.uint32))
+    for sign in (0, 0x80000000):
+        for b0 in range(lo, hi, 1 << 24):
+            cnt = min(1 << 24, hi - b0)
+            a = np.empty(cnt, np.uint8)
+            r = np.empty(cnt, np.uint8)
+            L.orc_e4m3_encode_range(b0 | sign, cnt, a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+            R.ref_e4m3_encode_range(b0 | sign, cnt, r.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+            assert int((a != r).sum()) == 0
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference lib/golden not built here")
+def test_bf16_rounding_vs_reference():
+    L, R = O.lib(), O.ref()
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(20000).astype(np.float32) * np.float32(1e3),
+                        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-45, 3.4e38], np.float32)])
+    x = np.ascontiguousarray(x)
+    r = np.empty(len(x), np.uint16)
+    R.ref_f32_to_bf16_array(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(x),
+                            r.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)))
+    got = np.array([L.orc_f32_to_bf16(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(got, r)
+
+
+def test_requant_postpass_vs_mx_golden_fixture():
+    """The reference CLI's MX_OUT_FMT=0 post-pass (mx_golden.cpp:146-190) on its own bf16 C."""
+    z = np.load(os.path.join(GOLD, "requant_postpass.npz"))
+    n = len([k for k in z.files if k.startswith("C")])
+    assert n >= 3
+    for i in range(n):
+        C = (z[f"C{i}"].astype(np.uint32) << 16).view(np.float32)
+        codes, scales = O.quantize_rows(C, O.FMT_E4M3)
+        np.testing.assert_array_equal(scales, z[f"scales{i}"])
+        np.testing.assert_array_equal(codes, z[f"codes{i}"])
+
+
+def test_scale_code_invariants():
+    """amax == 0 -> 0; otherwise amax / 2^(code-127) in [256, 512) (E4M3) / [16, 32) (E3M2)
+    except in the one-ulp log2f window just below a power of two, and clamped to [0, 254]."""
+    L = O.lib()
+    rng = np.random.default_rng(7)
+    assert L.orc_scale_code(0.0, 0) == 0 and L.orc_scale_code(0.0, 1) == 0
+    for a in (rng.standard_normal(5000).astype(np.float32) ** 2 * np.float32(2.0) ** rng.integers(-100, 100, 5000)):
+        if not np.isfinite(a) or a == 0:
+            continue
+        for fmt, lo in ((0, 256.0), (1, 16.0)):
+            c = L.orc_scale_code(float(a), fmt)
+            r = float(a) / 2.0 ** (c - 127)
+            if 0 < c < 254:
+                assert lo * (1 - 2 ** -20) <= r < 2 * lo
+    assert L.orc_scale_code(1e-42, 0) == 0 and L.orc_scale_code(3.0e38, 0) == 127 - 8 + 127
+
+
+def test_quantize_rows_cols_roundtrip_error_bound():
+    """Dequantized MX values are within half an E4M3 ulp (relative 2^-4) of the input for
+    elements within 2^-6 of the block scale range, and blocks are independent."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((64, 128)).astype(np.float32)
+    codes, scales = O.quantize_rows(x, O.FMT_E4M3)
+    L = O.lib()
+    scale = np.repeat(2.0 ** (scales.astype(np.float64) - 127), 32, axis=1)
+    dec = np.vectorize(lambda c: L.orc_e4m3_decode(int(c)))(codes) * scale
+    y = np.abs(x) / scale
+    normal = (y >= 2.0 ** -6) & (y <= 448.0)
+    assert np.all(np.abs(dec - x)[normal] <= np.abs(x)[normal] * 2.0 ** -4 + 1e-30)
+    sat = y > 464.0
+    assert np.all(np.abs(dec[sat]) == 448.0 * scale[sat])
+    assert np.all(dec[y < 2.0 ** -7] == 0.0)
+    # column blocking equals row blocking of the transpose
+    c2, s2 = O.quantize_cols(np.ascontiguousarray(x.T), O.FMT_E4M3)
+    np.testing.assert_array_equal(c2, codes.T)
+    np.testing.assert_array_equal(s2, scales.T)
