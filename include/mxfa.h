@@ -1,0 +1,134 @@
+/*
+ * mxfa.h -- C ABI of the MI355X (gfx950) MXFP8 flash-attention library (libmxfa.so).
+ *
+ * Replaces the operator surface of ucb-bar/radiance-kernels'
+ * kernels/flash_attention_mx{,_gqa,_gemma,_fp6,_stable}.  In the reference the
+ * "operator" is a compile-time specialised bare-metal program: operands and
+ * shape/causal/softcap/window parameters arrive as a generated header
+ * (kernels/flash_attention_mx_gqa/fa_gen_data.py:119-159,
+ * kernels/flash_attention_mx_gemma/fa_gen_data.py:165-182), the entry point is
+ * fa_entry(arg, tid, threads, threadblock) started by mu_schedule
+ * (kernels/flash_attention_mx_gqa/kernel.cpp:91-191, lib/include/mu_schedule.h:8-15)
+ * and the output is bf16 O at a fixed address (kernel.cpp:46-50,115).  Here the same
+ * operands (E4M3/E3M2 element codes + per-block-32 E8M0 scales) and parameters are
+ * passed at run time, and O is fp32.
+ *
+ * Conventions
+ *  - All tensors are caller-owned device memory; the library allocates nothing per
+ *    call (decode takes a caller workspace).  Element codes are one byte each
+ *    (E3M2 codes in the low 6 bits).  Base pointers must be 16-byte aligned.
+ *  - Calls are asynchronous on `stream` (a hipStream_t; NULL = default stream) and
+ *    never synchronize the host.  Results are deterministic (fixed reduction order,
+ *    no floating-point atomics).  Calls are thread-safe.
+ *  - Errors are returned as mxfa_status; mxfa_last_error() gives a thread-local
+ *    description.  Arguments are validated before any launch.
+ *
+ * Layouts (B batch, Hq query heads, Hkv KV heads, Sq queries, Sk keys, D head dim):
+ *   q   [B][Hq][Sq][D]   q_sc [B][Hq][Sq][D/32]     (32-blocks along D)
+ *   k   [B][Hkv][Sk][D]  k_sc [B][Hkv][Sk][D/32]    (32-blocks along D)
+ *   v   [B][Hkv][Sk][D]  v_sc [B][Hkv][Sk/32][D]    (32-blocks along the key axis,
+ *                         the reference's V_scales[Sk/32][d], flash_attention_mx/gen_data.py:118-119)
+ *   o   [B][Hq][Sq][D]   fp32
+ */
+#ifndef MXFA_H
+#define MXFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXFA_VERSION 1
+
+typedef enum {
+  MXFA_OK = 0,
+  MXFA_ERR_INVALID_ARG = 1,   /* bad shape, pointer, alignment or parameter */
+  MXFA_ERR_UNSUPPORTED = 2,   /* valid but not implemented (e.g. head_dim 96) */
+  MXFA_ERR_HIP = 3,           /* a HIP runtime call failed */
+  MXFA_ERR_MODULE = 4,        /* the gfx950 code object could not be loaded */
+  MXFA_ERR_WORKSPACE = 5      /* decode workspace missing or too small */
+} mxfa_status;
+
+typedef enum { MXFA_FMT_E4M3 = 0, MXFA_FMT_E3M2 = 1 } mxfa_fmt;
+
+/* Attention parameters (the reference's generated FA_* defines,
+ * kernels/flash_attention_mx_gemma/fa_gen_data.py:147-181). */
+typedef struct {
+  int32_t batch, num_q_heads, num_kv_heads; /* FA_NQ / FA_NKV; query head h reads KV head h / (Hq/Hkv) */
+  int32_t seq_q, seq_k;                     /* FA_SQ / FA_SK; seq_k % 32 == 0                            */
+  int32_t head_dim;                         /* FA_D: 64, 128 or 256                                       */
+  int32_t causal;                           /* key kpos masked when kpos > qpos                          */
+  int32_t q_pos0;                           /* FA_QPOS0: global position of query row 0 (>= 0)           */
+  int32_t window;                           /* FA_WINDOW: 0 = off; else kpos masked when kpos+window <= qpos */
+  float   softmax_scale;                    /* FA_SOFTMAX_SCALE (normally 1/sqrt(D))                     */
+  float   softcap;                          /* FA_ATTN_SOFTCAP: 0 = off; s <- cap*tanh(s/cap) after scale */
+  int32_t v_fmt;                            /* mxfa_fmt of V (Q and K are E4M3)                          */
+  int32_t block_n;                          /* FA_BK: online-softmax key block; 0 = default (64)         */
+} mxfa_attn_params;
+
+/* ---- MX quantization (rule of lib/golden/mx_golden.cpp:146-190 with the element
+ *      codes of lib/golden/mx_fp_math.h:205-225 (E4M3) and :266-335 (E3M2)) ---- */
+
+/* 32-blocks along each row of a rows x cols fp32 matrix (Q, K, KV-cache K).
+ * codes [rows][cols], scales [rows][cols/32]; cols % 32 == 0.
+ * Replaces the reference's offline mx_quantize_cols for Q and K
+ * (kernels/flash_attention_mx_gqa/flash_attention_model.py:68-73, fa_gen_data.py:95-117). */
+mxfa_status mxfa_quantize_rows(const float *x, int64_t rows, int32_t cols, mxfa_fmt fmt,
+                               uint8_t *codes, uint8_t *scales, void *stream);
+
+/* 32-blocks along the rows of each of `mats` rows x cols matrices (V, KV-cache V).
+ * codes [mats][rows][cols], scales [mats][rows/32][cols]; rows % 32 == 0, cols % 4 == 0.
+ * Replaces mx_quantize_cols(V.t()) of fa_gen_data.py:103-104. */
+mxfa_status mxfa_quantize_cols(const float *x, int64_t mats, int32_t rows, int32_t cols, mxfa_fmt fmt,
+                               uint8_t *codes, uint8_t *scales, void *stream);
+
+/* ---- attention ---- */
+
+/* Prefill / full attention.  Replaces fa_entry + mu_schedule of the reference FA
+ * kernels (kernels/flash_attention_mx_gqa/kernel.cpp:91-191,
+ * kernels/flash_attention_mx_gemma/kernel.cpp:124-213). */
+mxfa_status mxfa_prefill(const mxfa_attn_params *p,
+                         const uint8_t *q, const uint8_t *q_sc,
+                         const uint8_t *k, const uint8_t *k_sc,
+                         const uint8_t *v, const uint8_t *v_sc,
+                         float *o, void *stream);
+
+/* Split-KV decode plan for seq_q == 1 (q_pos0 is the query's position, normally
+ * seq_k - 1): keys are processed in independent chunks of *split_len keys (each a
+ * streaming pass with block_n-key blocks) merged by log-sum-exp.  The reference has
+ * no decode kernel; this is the same recurrence over a KV cache. */
+mxfa_status mxfa_decode_plan(const mxfa_attn_params *p, int32_t *split_len, size_t *workspace_bytes);
+
+mxfa_status mxfa_decode(const mxfa_attn_params *p,
+                        const uint8_t *q, const uint8_t *q_sc,
+                        const uint8_t *k_cache, const uint8_t *k_sc,
+                        const uint8_t *v_cache, const uint8_t *v_sc,
+                        float *o, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The attention kernels' P requantization routine on caller-supplied fp32 P
+ * (finite, >= 0), 32-blocks along rows: codes [rows][cols], scales [rows][cols/32].
+ * Replaces fused_softmax_requant's requant stage (kernels/flash_attention_mx_gqa/
+ * flash_mx_impl.hpp:315-394) with rule R1 (lib/golden/mx_golden.cpp:146-190);
+ * exposed so the routine can be checked bit-exactly in isolation. */
+mxfa_status mxfa_requant_p(const float *p, int64_t rows, int32_t cols,
+                           uint8_t *codes, uint8_t *scales, void *stream);
+
+/* Synthetic inputs: x[i] ~ N(0,1) (counter-based hash + Box-Muller), each element
+ * multiplied by outlier_mul with probability outlier_p.  Replaces make_inputs /
+ * make_inputs_gqa (kernels/flash_attention_mx_gqa/flash_attention_model.py:58-65,166-172). */
+mxfa_status mxfa_fill_normal(float *x, int64_t n, uint64_t seed, float outlier_p, float outlier_mul,
+                             void *stream);
+
+/* ---- library ---- */
+mxfa_status mxfa_init(void);                       /* load the code object on the current device */
+void        mxfa_shutdown(void);                   /* unload all modules                          */
+const char *mxfa_status_string(mxfa_status st);
+const char *mxfa_last_error(void);                 /* thread-local detail of the last failure      */
+int32_t     mxfa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MXFA_H */

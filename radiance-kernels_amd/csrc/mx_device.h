@@ -1,0 +1,138 @@
+// Device-side MX rules for gfx950 (CDNA4).
+//
+// Rule "R1" of the reference's lib/golden C code, bit-exact:
+//   block scale  : code = clamp(floor(log2f(amax)) - P + 127, 0, 254), P = 8 (E4M3)
+//                  or 4 (E3M2), amax == 0 -> 0        (lib/golden/mx_golden.cpp:169-174)
+//   E4M3 element : floor(log2f(|y|)) < -6 -> 0, > 8 -> +-448, else RNE to 3 mantissa
+//                  bits, saturating at 448           (lib/golden/mx_fp_math.h:205-225)
+//   E3M2 element : bf16 RNE, then RNE to E4M2, then the fixed E4M2 -> E3M2 value
+//                  map                                (lib/golden/mx_fp_math.h:11-28, 266-335)
+// floorf(log2f(x)) is reproduced from the exponent plus a per-binade mantissa
+// threshold (log2f rounds to float, so values just below 2^(e+1) give e+1).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "log2_table.h"
+
+namespace mxfa {
+
+__constant__ uint32_t c_log2_thr[256] = MXFA_LOG2_THR_INIT;
+__constant__ uint32_t c_log2_sub_thr[23] = MXFA_LOG2_SUB_THR_INIT;
+
+// F4M3: the smallest float whose floorf(log2f()) is >= -6.  Scaled E4M3 inputs
+// below it flush to 0 under R1.
+constexpr uint32_t kE4M3FlushBits = (120u << 23) | 0x7ffffeu;
+
+// floorf(log2f(x)) for finite x > 0 (x == 0 returns a large negative number).
+__device__ __forceinline__ int floor_log2f(float x) {
+  uint32_t b = __float_as_uint(x) & 0x7fffffffu;
+  uint32_t E = b >> 23, m = b & 0x7fffffu;
+  if (E == 0) {
+    if (m == 0) return -1024;
+    int p = 31 - __clz(m);
+    return p - 149 + (m >= c_log2_sub_thr[p] ? 1 : 0);
+  }
+  return (int)E - 127 + (m >= c_log2_thr[E] ? 1 : 0);
+}
+
+// E8M0 block scale code; amax = max |x| over the block (NaN already dropped by fmaxf).
+__device__ __forceinline__ uint32_t scale_code(float amax, int log2_pmax) {
+  if (!(amax > 0.0f) || __builtin_isinf(amax)) return 0u;
+  int s2 = floor_log2f(amax) - log2_pmax + 127;
+  return (uint32_t)(s2 < 0 ? 0 : (s2 > 254 ? 254 : s2));
+}
+
+// R1 E4M3 element code of an already scaled value (integer formulation).
+__device__ __forceinline__ uint32_t e4m3_code(float y) {
+  uint32_t b = __float_as_uint(y);
+  uint32_t a = b & 0x7fffffffu;
+  if (a == 0u || a >= 0x7f800000u) return 0u;
+  uint32_t s = (b >> 24) & 0x80u;
+  int E = floor_log2f(__uint_as_float(a));
+  if (E < -6) return 0u;
+  if (E > 8) return s | 0x7eu;
+  int q = 0;
+  if (E == (int)(a >> 23) - 127) {
+    uint32_t mant = a & 0x7fffffu;
+    q = (int)(mant >> 20);
+    uint32_t rem = mant & 0xfffffu;
+    q += (rem > 0x80000u || (rem == 0x80000u && (q & 1))) ? 1 : 0;
+    if (q == 8) { q = 0; E++; }
+  }
+  if (E > 8 || (E == 8 && q == 7)) return s | 0x7eu;
+  return s | ((uint32_t)(E + 7) << 3) | (uint32_t)q;
+}
+
+// lib/golden bf16 RNE (+-0 -> +0, tiny -> +0, NaN quieted).
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+  if (x == 0.0f) return 0u;
+  uint32_t b = __float_as_uint(x);
+  if (((b >> 23) & 0xffu) == 0xffu) {
+    uint32_t h = b >> 16;
+    if ((b & 0x7fffffu) && !(h & 0x40u)) h |= 0x40u;
+    return h & 0xffffu;
+  }
+  uint32_t r = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+  return (r & 0x7fffu) == 0u ? 0u : r;
+}
+
+// R1 E3M2 code (6 bits, one per byte) of a bf16 pattern.
+__device__ __forceinline__ uint32_t e3m2_code_bf16(uint32_t h) {
+  uint32_t neg = (h >> 15) & 1u;
+  int E = (int)((h >> 7) & 0xffu), M = (int)(h & 0x7fu);
+  if (E == 0) return 0u;
+  uint32_t c;
+  if (E == 255) {
+    c = 0x1fu;                                   // inf / NaN -> E4M2 inf -> +-28
+  } else {
+    int e = E - 127;
+    if (e > 7 || e < -6) return 0u;              // reference maps both tails to 0
+    int q = M >> 5, r = (M >> 4) & 1, st = (M & 15) != 0;
+    int sig = q + (r & (st | (q & 1)));
+    if (sig == 4) { sig = 0; e++; }
+    if (e >= 5) c = 0x1fu;                       // >= 32 (or E4M2 overflow) -> 28
+    else if (e >= -2) c = ((uint32_t)(e + 3) << 2) | (uint32_t)sig;
+    else if (e == -3) c = sig < 2 ? 2u : 3u;     // 0.125 / 0.1875
+    else if (e == -4) c = sig < 2 ? 1u : 2u;     // 0.0625 / 0.125
+    else return 0u;                              // <= 0.0546875
+  }
+  return (neg << 5) | c;
+}
+
+// E3M2 codes (low 6 bits of each byte) -> E4M3 codes of the same values (exact:
+// every E3M2 value is an E4M3 value), four per dword.
+__device__ __forceinline__ uint32_t e3m2x4_to_e4m3x4(uint32_t w) {
+  uint32_t x = w & 0x1f1f1f1fu;
+  uint32_t s = (w & 0x20202020u) << 2;
+  uint32_t nrm = (x + 0x10101010u) << 1;
+  uint32_t sub = __builtin_amdgcn_perm(0u, 0x24201800u, x);   // 0, 2^-4, 2^-3, 1.5*2^-3
+  uint32_t m = ((x & 0x1c1c1c1cu) + 0x7c7c7c7cu) & 0x80808080u;
+  uint32_t mask = m | (m - (m >> 7));
+  return ((nrm & mask) | (sub & ~mask)) | s;
+}
+
+// ---------------------------------------------------------------------------
+// Fast R1 requant of non-negative, finite fp32 values (the attention P tiles).
+// y = p * 2^(127 - sc) is exact (power-of-two scaling of a value below 512);
+// R1 flushes y below F4M3 and saturates at 448; in between the hardware
+// conversion (RNE, OCP E4M3) gives the R1 code, including for y just below a
+// power of two where log2f rounds up.
+// ---------------------------------------------------------------------------
+typedef short v2s_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float r1_prep(float p, int sh) {
+  float y = __builtin_ldexpf(p, sh);
+  y = y < __uint_as_float(kE4M3FlushBits) ? 0.0f : y;
+  return __builtin_fminf(y, 448.0f);
+}
+
+__device__ __forceinline__ uint32_t r1_pack4(float p0, float p1, float p2, float p3, int sh) {
+  v2s_t pk = {0, 0};
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, r1_prep(p0, sh), r1_prep(p1, sh), 1.0f, false);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, r1_prep(p2, sh), r1_prep(p3, sh), 1.0f, true);
+  return (uint32_t)(uint16_t)pk[0] | ((uint32_t)(uint16_t)pk[1] << 16);
+}
+
+}  // namespace mxfa

@@ -1,0 +1,330 @@
+// libmxfa.so: C ABI over the gfx950 code object mxfa_kernels.hsaco.
+//
+// Replaces the reference's launch path (mu_schedule(fa_entry, nullptr, occupancy),
+// lib/src/mu_schedule.cpp:83-104, started from main() in
+// kernels/flash_attention_mx_gqa/kernel.cpp:186-191) with hipModuleLaunchKernel on
+// the caller's stream.  One hipModule per device is loaded lazily (or by
+// mxfa_init) and kept until mxfa_shutdown.  Host code only: built with g++ against
+// libamdhip64; the kernels are compiled separately by hipcc --genco.
+#include "mxfa.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "mxfa_args.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+mxfa_status fail(mxfa_status st, const std::string& msg) {
+  g_err = msg;
+  return st;
+}
+
+#define MXFA_HIP(call)                                                                         \
+  do {                                                                                         \
+    hipError_t e_ = (call);                                                                    \
+    if (e_ != hipSuccess) return fail(MXFA_ERR_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+const char* const kKernelNames[] = {
+    "mxfa_quant_rows_e4m3",    "mxfa_quant_rows_e3m2",    "mxfa_quant_cols_e4m3", "mxfa_quant_cols_e3m2",
+    "mxfa_requant_p_rows",     "mxfa_fill_normal_f32",    "mxfa_prefill_d64",     "mxfa_prefill_d128",
+    "mxfa_prefill_d256",       "mxfa_prefill_d64_softcap", "mxfa_prefill_d128_softcap", "mxfa_prefill_d256_softcap",
+    "mxfa_decode_d64",         "mxfa_decode_d128",        "mxfa_decode_d256",     "mxfa_decode_d64_softcap",
+    "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine",
+};
+constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
+
+struct DeviceModule {
+  hipModule_t mod = nullptr;
+  hipFunction_t fn[kNumKernels] = {};
+};
+
+std::mutex g_mu;
+std::unordered_map<int, DeviceModule> g_mods;
+
+std::string code_object_path() {
+  if (const char* env = getenv("MXFA_HSACO")) return env;
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&mxfa_version), &info) && info.dli_fname) {
+    std::string p(info.dli_fname);
+    size_t slash = p.rfind('/');
+    return (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) + "/mxfa_kernels.hsaco";
+  }
+  return "mxfa_kernels.hsaco";
+}
+
+// Module of the current device (loaded on first use).
+mxfa_status module_for_current(DeviceModule** out) {
+  int dev = -1;
+  MXFA_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_mods.find(dev);
+  if (it != g_mods.end()) {
+    *out = &it->second;
+    return MXFA_OK;
+  }
+  hipDeviceProp_t prop;
+  MXFA_HIP(hipGetDeviceProperties(&prop, dev));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(MXFA_ERR_UNSUPPORTED, std::string("device ") + std::to_string(dev) + " is " + prop.gcnArchName +
+                                          "; libmxfa is built for gfx950 (MI355X) only");
+  DeviceModule dm;
+  std::string path = code_object_path();
+  hipError_t e = hipModuleLoad(&dm.mod, path.c_str());
+  if (e != hipSuccess) return fail(MXFA_ERR_MODULE, "hipModuleLoad(" + path + "): " + hipGetErrorString(e));
+  for (int i = 0; i < kNumKernels; i++) {
+    e = hipModuleGetFunction(&dm.fn[i], dm.mod, kKernelNames[i]);
+    if (e != hipSuccess) {
+      (void)hipModuleUnload(dm.mod);
+      return fail(MXFA_ERR_MODULE, std::string("kernel ") + kKernelNames[i] + " missing from " + path);
+    }
+  }
+  auto res = g_mods.emplace(dev, dm);
+  *out = &res.first->second;
+  return MXFA_OK;
+}
+
+hipFunction_t fn_by_name(DeviceModule* dm, const char* name) {
+  for (int i = 0; i < kNumKernels; i++)
+    if (std::strcmp(kKernelNames[i], name) == 0) return dm->fn[i];
+  return nullptr;
+}
+
+mxfa_status launch(DeviceModule* dm, const char* name, dim3 grid, dim3 block, void** args, void* stream) {
+  hipFunction_t f = fn_by_name(dm, name);
+  if (!f) return fail(MXFA_ERR_MODULE, std::string("unknown kernel ") + name);
+  MXFA_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+                                 reinterpret_cast<hipStream_t>(stream), args, nullptr));
+  return MXFA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
+  if (!p) return fail(MXFA_ERR_INVALID_ARG, "params is NULL");
+  if (p->batch < 1 || p->num_q_heads < 1 || p->num_kv_heads < 1 || p->seq_q < 1 || p->seq_k < 1)
+    return fail(MXFA_ERR_INVALID_ARG, "batch, heads, seq_q and seq_k must be >= 1");
+  if (p->num_q_heads % p->num_kv_heads)
+    return fail(MXFA_ERR_INVALID_ARG, "num_q_heads must be a multiple of num_kv_heads");
+  if (p->head_dim % 32) return fail(MXFA_ERR_INVALID_ARG, "head_dim must be a multiple of 32");
+  if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
+    return fail(MXFA_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (p->seq_k % 32) return fail(MXFA_ERR_INVALID_ARG, "seq_k must be a multiple of 32 (V scale blocks)");
+  if (p->q_pos0 < 0 || p->window < 0) return fail(MXFA_ERR_INVALID_ARG, "q_pos0 and window must be >= 0");
+  if (!(p->softmax_scale > 0.0f) || !std::isfinite(p->softmax_scale))
+    return fail(MXFA_ERR_INVALID_ARG, "softmax_scale must be finite and > 0");
+  if (!(p->softcap >= 0.0f) || !std::isfinite(p->softcap)) return fail(MXFA_ERR_INVALID_ARG, "softcap must be finite and >= 0");
+  if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "v_fmt must be E4M3 or E3M2");
+  if (p->block_n != 0 && p->block_n != 64) return fail(MXFA_ERR_UNSUPPORTED, "block_n must be 0 (default) or 64");
+  if (decode) {
+    if (p->seq_q != 1) return fail(MXFA_ERR_INVALID_ARG, "decode needs seq_q == 1");
+    if (p->num_q_heads / p->num_kv_heads > 32)
+      return fail(MXFA_ERR_UNSUPPORTED, "decode supports at most 32 query heads per KV head");
+  }
+  int64_t qelems = (int64_t)p->batch * p->num_q_heads * p->seq_q * p->head_dim;
+  int64_t kelems = (int64_t)p->batch * p->num_kv_heads * p->seq_k * p->head_dim;
+  if (qelems > (int64_t)1 << 40 || kelems > (int64_t)1 << 40) return fail(MXFA_ERR_INVALID_ARG, "tensor too large");
+  return MXFA_OK;
+}
+
+mxfa_status check_ptrs(const void* const* ptrs, int n) {
+  for (int i = 0; i < n; i++) {
+    if (!ptrs[i]) return fail(MXFA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (!aligned16(ptrs[i])) return fail(MXFA_ERR_INVALID_ARG, "tensor pointers must be 16-byte aligned");
+  }
+  return MXFA_OK;
+}
+
+FaArgs make_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* qs, const uint8_t* k, const uint8_t* ks,
+                 const uint8_t* v, const uint8_t* vs, float* o) {
+  FaArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.q = q; a.qs = qs; a.k = k; a.ks = ks; a.v = v; a.vs = vs; a.o = o;
+  a.B = p->batch; a.Hq = p->num_q_heads; a.Hkv = p->num_kv_heads; a.Sq = p->seq_q; a.Sk = p->seq_k;
+  a.q_pos0 = p->q_pos0; a.window = p->window; a.causal = p->causal ? 1 : 0; a.v_e3m2 = p->v_fmt == MXFA_FMT_E3M2;
+  a.group = p->num_q_heads / p->num_kv_heads;
+  const float log2e = 1.4426950408889634f;
+  a.c_log2 = p->softmax_scale * log2e;
+  if (p->softcap > 0.0f) {
+    a.sc_u = p->softmax_scale / p->softcap;
+    a.cap_log2 = p->softcap * log2e;
+  }
+  return a;
+}
+
+const char* kernel_name(const char* kind, int D, bool softcap) {
+  static thread_local char buf[64];
+  std::snprintf(buf, sizeof buf, "mxfa_%s_d%d%s", kind, D, softcap ? "_softcap" : "");
+  return buf;
+}
+
+// Decode geometry: chunks of split_len keys (multiple of 64) so that the whole
+// call has about 16K waves in flight.
+void decode_geometry(const mxfa_attn_params* p, int* split_len, int* nparts) {
+  int64_t bk = (int64_t)p->batch * p->num_kv_heads;
+  int64_t target = (16384 + bk - 1) / bk;
+  if (target < 1) target = 1;
+  int64_t len = (p->seq_k + target - 1) / target;
+  len = (len + 63) / 64 * 64;
+  if (len < 64) len = 64;
+  *split_len = (int)len;
+  *nparts = (int)((p->seq_k + len - 1) / len);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t mxfa_version(void) { return MXFA_VERSION; }
+
+const char* mxfa_status_string(mxfa_status st) {
+  switch (st) {
+    case MXFA_OK: return "ok";
+    case MXFA_ERR_INVALID_ARG: return "invalid argument";
+    case MXFA_ERR_UNSUPPORTED: return "unsupported";
+    case MXFA_ERR_HIP: return "HIP error";
+    case MXFA_ERR_MODULE: return "code object error";
+    case MXFA_ERR_WORKSPACE: return "workspace too small";
+  }
+  return "unknown status";
+}
+
+const char* mxfa_last_error(void) { return g_err.c_str(); }
+
+mxfa_status mxfa_init(void) {
+  DeviceModule* dm;
+  return module_for_current(&dm);
+}
+
+void mxfa_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto& kv : g_mods) (void)hipModuleUnload(kv.second.mod);
+  g_mods.clear();
+}
+
+mxfa_status mxfa_quantize_rows(const float* x, int64_t rows, int32_t cols, mxfa_fmt fmt, uint8_t* codes,
+                               uint8_t* scales, void* stream) {
+  if (rows < 0 || cols <= 0 || cols % 32) return fail(MXFA_ERR_INVALID_ARG, "cols must be a positive multiple of 32");
+  if (fmt != MXFA_FMT_E4M3 && fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad fmt");
+  if (rows == 0) return MXFA_OK;
+  if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
+    return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte and codes 4-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  int64_t nblocks = rows * (int64_t)cols / 32;
+  int64_t threads = nblocks * 8;
+  dim3 grid((unsigned)((threads + 255) / 256));
+  void* args[] = {(void*)&x, &nblocks, &codes, &scales};
+  return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_rows_e4m3" : "mxfa_quant_rows_e3m2", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32_t cols, mxfa_fmt fmt, uint8_t* codes,
+                               uint8_t* scales, void* stream) {
+  if (mats < 0 || rows <= 0 || rows % 32 || cols <= 0 || cols % 4)
+    return fail(MXFA_ERR_INVALID_ARG, "rows must be a positive multiple of 32 and cols of 4");
+  if (fmt != MXFA_FMT_E4M3 && fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad fmt");
+  if (mats == 0) return MXFA_OK;
+  if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u) || (reinterpret_cast<uintptr_t>(scales) & 3u))
+    return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte, codes and scales 4-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  int64_t threads = mats * (rows / 32) * (cols / 4);
+  dim3 grid((unsigned)((threads + 255) / 256));
+  void* args[] = {(void*)&x, &mats, &rows, &cols, &codes, &scales};
+  return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : "mxfa_quant_cols_e3m2", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_requant_p(const float* p, int64_t rows, int32_t cols, uint8_t* codes, uint8_t* scales, void* stream) {
+  if (rows < 0 || cols <= 0 || cols % 32) return fail(MXFA_ERR_INVALID_ARG, "cols must be a positive multiple of 32");
+  if (rows == 0) return MXFA_OK;
+  if (!p || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  if (!aligned16(p) || (reinterpret_cast<uintptr_t>(codes) & 3u))
+    return fail(MXFA_ERR_INVALID_ARG, "p must be 16-byte and codes 4-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  int64_t nblocks = rows * (int64_t)cols / 32;
+  dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
+  void* args[] = {(void*)&p, &nblocks, &codes, &scales};
+  return launch(dm, "mxfa_requant_p_rows", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p, float outlier_mul, void* stream) {
+  if (n < 0) return fail(MXFA_ERR_INVALID_ARG, "n must be >= 0");
+  if (n == 0) return MXFA_OK;
+  if (!x) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  dim3 grid((unsigned)((n + 255) / 256));
+  void* args[] = {&x, &n, &seed, &outlier_p, &outlier_mul};
+  return launch(dm, "mxfa_fill_normal_f32", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
+                         const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* stream) {
+  if (mxfa_status st = check_params(p, false)) return st;
+  const void* ptrs[] = {q, q_sc, k, k_sc, v, v_sc, o};
+  if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  FaArgs a = make_args(p, q, q_sc, k, k_sc, v, v_sc, o);
+  a.hpw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
+  a.qpw = 32 * (4 / a.hpw);
+  a.n_qblk = (p->seq_q + a.qpw - 1) / a.qpw;
+  dim3 grid((unsigned)a.n_qblk, (unsigned)(p->batch * p->num_kv_heads * (a.group / a.hpw)));
+  void* args[] = {&a};
+  return launch(dm, kernel_name("prefill", p->head_dim, p->softcap > 0.0f), grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* split_len, size_t* workspace_bytes) {
+  if (mxfa_status st = check_params(p, true)) return st;
+  int sl, np;
+  decode_geometry(p, &sl, &np);
+  if (split_len) *split_len = sl;
+  if (workspace_bytes)
+    *workspace_bytes = (size_t)p->batch * p->num_q_heads * np * (p->head_dim + 2) * sizeof(float) + 256;
+  return MXFA_OK;
+}
+
+mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k_cache,
+                        const uint8_t* k_sc, const uint8_t* v_cache, const uint8_t* v_sc, float* o, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (mxfa_status st = check_params(p, true)) return st;
+  const void* ptrs[] = {q, q_sc, k_cache, k_sc, v_cache, v_sc, o};
+  if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
+  size_t need = 0;
+  int32_t sl = 0;
+  mxfa_decode_plan(p, &sl, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(MXFA_ERR_WORKSPACE, "decode workspace must be at least " + std::to_string(need) + " bytes");
+  if (!aligned16(workspace)) return fail(MXFA_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  FaArgs a = make_args(p, q, q_sc, k_cache, k_sc, v_cache, v_sc, o);
+  int split_len, nparts;
+  decode_geometry(p, &split_len, &nparts);
+  a.split_len = split_len;
+  a.n_qblk = nparts;
+  int64_t nbh = (int64_t)p->batch * p->num_q_heads;
+  a.part_o = reinterpret_cast<float*>(workspace);
+  a.part_ml = a.part_o + nbh * nparts * p->head_dim;
+  const int nw = p->head_dim == 256 ? 2 : 4;   // waves per decode workgroup (LDS-limited at D = 256)
+  dim3 grid((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads));
+  void* args[] = {&a};
+  if (mxfa_status st = launch(dm, kernel_name("decode", p->head_dim, p->softcap > 0.0f), grid, dim3(64 * nw), args, stream))
+    return st;
+  return launch(dm, "mxfa_decode_combine", dim3((unsigned)nbh), dim3((unsigned)p->head_dim), args, stream);
+}
+
+}  // extern "C"

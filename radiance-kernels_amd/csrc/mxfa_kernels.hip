@@ -1,0 +1,675 @@
+// MXFP8 flash attention for MI355X (gfx950): quantizers, prefill, split-KV decode.
+//
+// Built with `hipcc --genco --offload-arch=gfx950` into mxfa_kernels.hsaco and
+// launched by mxfa_host.cpp through hipModuleLaunchKernel.  Every entry point is
+// extern "C" so the host looks it up by name.
+//
+// Reference path (ucb-bar/radiance-kernels): kernels/flash_attention_mx{,_gqa,
+// _gemma,_fp6,_stable}.  Per key block the reference runs QK^T on the MX mesh,
+// an online softmax + MX requant of P on the SIMT cores, then PV on the mesh and
+// a rescale of the O accumulator (kernels/flash_attention_mx_gqa/kernel.cpp:124-175,
+// flash_mx_impl.hpp:315-553).  Here both products run on scaled MFMA
+// (v_mfma_scale_f32_32x32x64_f8f6f4) and the softmax/requant on the VALU.
+//
+// Scaled-MFMA operand layout (32x32x64, fp8), measured on gfx950:
+//   A (32 rows x 64 k): lane l holds row l%32; byte j of its 32 bytes is
+//       k = 32*(j/16) + 16*(l/32) + j%16; the lane's scale applies to row l%32,
+//       k-block l/32 (k in [32*(l/32), 32*(l/32)+32)).
+//   B (64 k x 32 cols): lane l holds col l%32, same k mapping and scale rule.
+//   C (32x32 fp32): lane l, reg i -> col l%32, row 8*(i/4) + 4*(l/32) + i%4.
+// Attention computes S^T = K Q^T so a lane owns one query and 16 keys of every
+// 32-key tile, which makes the per-(query, 32 keys) P scale a lane-pair
+// reduction; O^T += V^T P^T then takes P straight from registers (B) and V^T
+// from LDS through ds_read_b64_tr_b8 (A), with the key order of both operands
+// matched to the S^T register order.
+//
+// Precision.  The scaled fp8 MFMA sums each group of 8 products in a fixed-point
+// window of 14 significant bits below the group's largest product (measured on
+// gfx950), so scores carry ~1e-3 relative error; R1's floor(log2(amax)) P scale
+// turns such perturbations into whole-block requantization changes.  The scores
+// are therefore computed on the bf16 MFMA (v_mfma_f32_32x32x16_bf16, fp32-exact
+// accumulation) from the MX operands dequantized exactly into bf16 (E4M3 x 2^k is a
+// bf16 value), while PV -- whose P operand is MX-quantized by definition -- runs on
+// the scaled MXFP8 MFMA.  bf16 MFMA layout (32x32x16): lane l holds row/col l%32,
+// k = 8*(l/32) + j for its 8 elements; C as above.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mx_device.h"
+#include "mxfa_args.h"
+
+using namespace mxfa;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+#define LOG2E_F 1.4426950408889634f
+
+// ============================================================================
+// Quantizers (rule R1).  One MX block of 32 values is handled by 8 lanes.
+// ============================================================================
+template <int FMT>
+__device__ __forceinline__ uint32_t encode4(float4 v, int sh) {
+  float y[4] = {__builtin_ldexpf(v.x, sh), __builtin_ldexpf(v.y, sh), __builtin_ldexpf(v.z, sh),
+                __builtin_ldexpf(v.w, sh)};
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    uint32_t c = FMT == 0 ? e4m3_code(y[i]) : e3m2_code_bf16(bf16_rne(y[i]));
+    w |= c << (8 * i);
+  }
+  return w;
+}
+
+// x: rows of `cols` floats, 32-blocks along the row. nblocks = rows * cols / 32.
+template <int FMT>
+__device__ void quant_rows_impl(const float* __restrict__ x, int64_t nblocks, uint8_t* __restrict__ codes,
+                                uint8_t* __restrict__ scales) {
+  int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t blk = gt >> 3;
+  int part = (int)(gt & 7);
+  if (blk >= nblocks) return;                       // whole 8-lane groups leave together
+  float4 v = reinterpret_cast<const float4*>(x)[blk * 8 + part];
+  float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  a = fmaxf(a, __shfl_xor(a, 4));
+  uint32_t sc = scale_code(a, FMT == 0 ? 8 : 4);
+  reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = encode4<FMT>(v, 127 - (int)sc);
+  if (part == 0) scales[blk] = (uint8_t)sc;
+}
+
+extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_e4m3(const float* x, int64_t nblocks,
+                                                                       uint8_t* codes, uint8_t* scales) {
+  quant_rows_impl<0>(x, nblocks, codes, scales);
+}
+extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_e3m2(const float* x, int64_t nblocks,
+                                                                       uint8_t* codes, uint8_t* scales) {
+  quant_rows_impl<1>(x, nblocks, codes, scales);
+}
+
+// 32-blocks along rows (V layout): each lane owns 4 adjacent columns of one
+// 32-row block.  mats matrices of rows x cols; rows % 32 == 0, cols % 4 == 0.
+template <int FMT>
+__device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int rows, int cols,
+                                uint8_t* __restrict__ codes, uint8_t* __restrict__ scales) {
+  int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int cg = cols / 4;
+  int64_t per_mat = (int64_t)(rows / 32) * cg;
+  if (gt >= mats * per_mat) return;
+  int64_t m = gt / per_mat;
+  int64_t rem = gt % per_mat;
+  int rb = (int)(rem / cg), c4 = (int)(rem % cg) * 4;
+  const float* base = x + (m * rows + (int64_t)rb * 32) * cols + c4;
+  float4 amax = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < 32; r++) {
+    float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
+    amax.x = fmaxf(amax.x, fabsf(v.x)); amax.y = fmaxf(amax.y, fabsf(v.y));
+    amax.z = fmaxf(amax.z, fabsf(v.z)); amax.w = fmaxf(amax.w, fabsf(v.w));
+  }
+  const int lp = FMT == 0 ? 8 : 4;
+  uint32_t s0 = scale_code(amax.x, lp), s1 = scale_code(amax.y, lp), s2 = scale_code(amax.z, lp),
+           s3 = scale_code(amax.w, lp);
+  uint8_t* cbase = codes + (m * rows + (int64_t)rb * 32) * cols + c4;
+  for (int r = 0; r < 32; r++) {
+    float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
+    float y0 = __builtin_ldexpf(v.x, 127 - (int)s0), y1 = __builtin_ldexpf(v.y, 127 - (int)s1);
+    float y2 = __builtin_ldexpf(v.z, 127 - (int)s2), y3 = __builtin_ldexpf(v.w, 127 - (int)s3);
+    uint32_t w;
+    if (FMT == 0)
+      w = e4m3_code(y0) | (e4m3_code(y1) << 8) | (e4m3_code(y2) << 16) | (e4m3_code(y3) << 24);
+    else
+      w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
+          (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);
+    *reinterpret_cast<uint32_t*>(cbase + (int64_t)r * cols) = w;
+  }
+  *reinterpret_cast<uint32_t*>(scales + (m * (rows / 32) + rb) * cols + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
+}
+
+extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e4m3(const float* x, int64_t mats, int rows, int cols,
+                                                                       uint8_t* codes, uint8_t* scales) {
+  quant_cols_impl<0>(x, mats, rows, cols, codes, scales);
+}
+extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e3m2(const float* x, int64_t mats, int rows, int cols,
+                                                                       uint8_t* codes, uint8_t* scales) {
+  quant_cols_impl<1>(x, mats, rows, cols, codes, scales);
+}
+
+// The attention kernels' P requant routine on caller-supplied fp32 P (>= 0,
+// finite), 32-blocks along rows: used by the tests to pin it bit-exactly.
+extern "C" __global__ void __launch_bounds__(256) mxfa_requant_p_rows(const float* p, int64_t nblocks,
+                                                                      uint8_t* codes, uint8_t* scales) {
+  int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t blk = gt >> 3;
+  int part = (int)(gt & 7);
+  if (blk >= nblocks) return;
+  float4 v = reinterpret_cast<const float4*>(p)[blk * 8 + part];
+  float a = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  a = fmaxf(a, __shfl_xor(a, 4));
+  uint32_t sc = scale_code(a, 8);
+  reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = r1_pack4(v.x, v.y, v.z, v.w, 127 - (int)sc);
+  if (part == 0) scales[blk] = (uint8_t)sc;
+}
+
+// ============================================================================
+// Synthetic inputs: x[i] ~ N(0,1) from a counter-based hash (splitmix64) and
+// Box-Muller; each element independently multiplied by `mul` with probability p.
+// ============================================================================
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+extern "C" __global__ void __launch_bounds__(256) mxfa_fill_normal_f32(float* x, int64_t n, uint64_t seed,
+                                                                       float outlier_p, float outlier_mul) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint64_t h = splitmix64(seed * 0x2545f4914f6cdd1dull + (uint64_t)i);
+  float u1 = ((float)(uint32_t)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  float u2 = (float)(uint32_t)((h >> 16) & 0xffffffu) * (1.0f / 16777216.0f);
+  float r = sqrtf(-2.0f * logf(u1));
+  float z = r * cosf(6.283185307179586f * u2);
+  if (outlier_p > 0.0f) {
+    uint64_t h2 = splitmix64(h ^ 0xa0761d6478bd642full);
+    float u3 = (float)(uint32_t)(h2 >> 40) * (1.0f / 16777216.0f);
+    if (u3 < outlier_p) z *= outlier_mul;
+  }
+  x[i] = z;
+}
+
+// ============================================================================
+// Attention
+// ============================================================================
+// FaArgs: see mxfa_args.h
+
+
+constexpr int BN = 64;          // online-softmax key block (the reference's Bk)
+constexpr int NWAVE = 4;
+
+__device__ __forceinline__ v16f mfma_mx(v8i a, v8i b, v16f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+__device__ __forceinline__ v16f mfma_bf16(v4i a, v4i b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+}
+
+// 8 E4M3 codes (two dwords) x 2^(sc-127) -> 8 bf16 (exact), in element order.
+__device__ __forceinline__ v4i fp8x8_to_bf16x8(uint32_t w0, uint32_t w1, float scale) {
+  v4i o;
+  o[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false));
+  o[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true));
+  o[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, false));
+  o[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, true));
+  return o;
+}
+
+// E8M0 code -> the float whose exponent field carries it (the scaled-convert operand).
+__device__ __forceinline__ float e8m0_as_float(uint32_t code) { return __uint_as_float(code << 23); }
+
+__device__ __forceinline__ v8i cat44(v4i lo, v4i hi) {
+  return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Per-tile staging of one key block: K and V codes (BN x D) and their scales.
+template <int D>
+struct BlockRegs {
+  static constexpr int CPR = D / 16;                 // 16-byte chunks per row
+  static constexpr int NCH = BN * CPR;               // chunks per matrix
+  static constexpr int PER = NCH / (NWAVE * 64);     // chunks per thread (2, 4 or 8 with 256 threads... )
+  static constexpr int SCH = BN * D / 32 / 16;       // 16-byte scale chunks per matrix
+  v4i k[PER > 0 ? PER : 1];
+  uint32_t kscale[PER > 0 ? PER : 1];   // E8M0 scale of each K chunk's 32-block
+  v4i v[PER > 0 ? PER : 1];
+  v4i vsc;
+};
+
+// LDS tiles: K as bf16 (row pitch 2D + 16 bytes), V as fp8 codes (pitch D + 16);
+// the 16-byte pads keep row starts on distinct banks.
+template <int D> struct Lds {
+  static constexpr int KP = D + 16;          // V row pitch (bytes)
+  static constexpr int KPB = 2 * D + 16;     // K (bf16) row pitch (bytes)
+  static constexpr int TILE = BN * KP;
+  static constexpr int TILEK = BN * KPB;
+  static constexpr int SC = BN * D / 32;
+};
+
+// Global -> registers for key block starting at key0 (rows >= Sk read as 0).
+template <int D>
+__device__ __forceinline__ void load_block(BlockRegs<D>& r, const uint8_t* __restrict__ kb, const uint8_t* __restrict__ ksb,
+                                           const uint8_t* __restrict__ vb, const uint8_t* __restrict__ vsb,
+                                           int key0, int Sk, int tid) {
+  constexpr int CPR = BlockRegs<D>::CPR;
+#pragma unroll
+  for (int i = 0; i < BlockRegs<D>::PER; i++) {
+    int c = tid + i * NWAVE * 64;
+    int row = c / CPR, col = (c % CPR) * 16;
+    int key = key0 + row;
+    v4i zk = {0, 0, 0, 0}, zv = {0, 0, 0, 0};
+    uint32_t ksc = 0;
+    if (key < Sk) {
+      zk = *reinterpret_cast<const v4i*>(kb + (int64_t)key * D + col);
+      zv = *reinterpret_cast<const v4i*>(vb + (int64_t)key * D + col);
+      ksc = ksb[(int64_t)key * (D / 32) + col / 32];
+    }
+    r.k[i] = zk;
+    r.kscale[i] = ksc;
+    r.v[i] = zv;
+  }
+  constexpr int SCH = BlockRegs<D>::SCH;
+  r.vsc = (v4i){0, 0, 0, 0};
+  if (tid < SCH) {
+    int byte = tid * 16;                        // V scales: [key/32][D]
+    int kb32 = key0 / 32 + byte / D;
+    if (kb32 < Sk / 32) r.vsc = *reinterpret_cast<const v4i*>(vsb + (int64_t)(key0 / 32) * D + byte);
+  }
+}
+
+// Registers -> LDS: K dequantized to bf16, V codes (E3M2 widened to E4M3), V scales.
+template <int D>
+__device__ __forceinline__ void store_block(const BlockRegs<D>& r, uint8_t* sKb, uint8_t* sV, uint8_t* sVs, int tid,
+                                            int v_e3m2) {
+  constexpr int CPR = BlockRegs<D>::CPR;
+  constexpr int KP = Lds<D>::KP;
+  constexpr int KPB = Lds<D>::KPB;
+#pragma unroll
+  for (int i = 0; i < BlockRegs<D>::PER; i++) {
+    int c = tid + i * NWAVE * 64;
+    int row = c / CPR, col = (c % CPR) * 16;
+    float sc = e8m0_as_float(r.kscale[i]);
+    v4i b0 = fp8x8_to_bf16x8((uint32_t)r.k[i][0], (uint32_t)r.k[i][1], sc);
+    v4i b1 = fp8x8_to_bf16x8((uint32_t)r.k[i][2], (uint32_t)r.k[i][3], sc);
+    *reinterpret_cast<v4i*>(sKb + row * KPB + col * 2) = b0;
+    *reinterpret_cast<v4i*>(sKb + row * KPB + col * 2 + 16) = b1;
+    v4i vv = r.v[i];
+    if (v_e3m2) {
+#pragma unroll
+      for (int w = 0; w < 4; w++) vv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)vv[w]);
+    }
+    *reinterpret_cast<v4i*>(sV + row * KP + col) = vv;
+  }
+  constexpr int SCH = BlockRegs<D>::SCH;
+  if (tid < SCH) *reinterpret_cast<v4i*>(sVs + tid * 16) = r.vsc;
+}
+
+// Per-wave online-softmax state and O accumulator for 32 query columns.
+template <int D>
+struct WaveState {
+  v16f o[D / 32];
+  float m;       // running max (in x units), per lane = per query
+  float l;       // per-lane partial row sum (the partner lane holds the rest)
+};
+
+// One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
+// mask: 0 = every key visible for every query of the wave; 1 = evaluate the mask.
+template <int D, bool SOFTCAP>
+__device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
+                                           const uint8_t* sVs, int key0, int qpos, bool qvalid, bool mask,
+                                           const FaArgs& a, int lane) {
+  constexpr int KP = Lds<D>::KP;
+  constexpr int KPB = Lds<D>::KPB;
+  constexpr int NT = BN / 32;
+  const int r = lane & 31, h = lane >> 5;
+
+  // ---- S^T = K Q^T (bf16 MFMA): tile t covers keys key0 + 32t .. +31
+  v16f s[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    s[t] = (v16f){};
+    const uint8_t* krow = sKb + (t * 32 + r) * KPB + 16 * h;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; kk++)
+      s[t] = mfma_bf16(*reinterpret_cast<const v4i*>(krow + 32 * kk), qb[kk], s[t]);
+  }
+
+  // ---- scores in log2 units (softcap) or raw units, masked -> -inf
+  float tmax[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float x = s[t][i];
+      if (SOFTCAP) {
+        float u = x * a.sc_u;
+        float e = __builtin_amdgcn_exp2f(-2.0f * LOG2E_F * fabsf(u));
+        float th = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+        x = a.cap_log2 * (u < 0.0f ? -th : th);
+      }
+      if (mask) {
+        int kpos = key0 + 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
+        bool vis = qvalid && kpos < a.Sk && (!a.causal || kpos <= qpos) && (a.window <= 0 || kpos + a.window > qpos);
+        x = vis ? x : -INFINITY;
+      }
+      s[t][i] = x;
+      mx = fmaxf(mx, x);
+    }
+    tmax[t] = mx;
+  }
+  // block (query, 32-key tile) maxima: combine the lane pair (l, l^32)
+  float bmax[NT];
+  float rmax = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    bmax[t] = fmaxf(tmax[t], __shfl_xor(tmax[t], 32));
+    rmax = fmaxf(rmax, bmax[t]);
+  }
+  // P = exp2((x - m) * c): the row maximum gets exactly exp2(0) = 1, like the
+  // reference's exp(S - m); a fused x*c - m*c would leave a rounding residue there
+  // that can move the block's power-of-two scale.
+  const float c = SOFTCAP ? 1.0f : a.c_log2;
+  float m_new = fmaxf(st.m, rmax);
+  float mu = m_new == -INFINITY ? 0.0f : m_new;
+  float corr = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((st.m - mu) * c);
+  st.m = m_new;
+
+  // ---- P and the per-tile amax from the tile max (subtract, scale and exp2 are monotone)
+  float lsum = 0.0f;
+  uint32_t pc[NT][4];
+  int psc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    float amax = __builtin_amdgcn_exp2f((bmax[t] - mu) * c);
+    uint32_t sc = scale_code(amax, 8);
+    int sh = 127 - (int)sc;
+    psc[t] = (int)sc;
+    float p[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      p[i] = __builtin_amdgcn_exp2f((s[t][i] - mu) * c);
+      lsum += p[i];
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) pc[t][g] = r1_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], sh);
+  }
+  st.l = st.l * corr + lsum;
+
+  // ---- O^T = O^T * corr + V^T P^T
+#pragma unroll
+  for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) st.o[dt][i] *= corr;
+
+  const int l16 = lane & 15, g16 = lane >> 4;
+#pragma unroll
+  for (int kstep = 0; kstep < BN / 64; kstep++) {
+    v8i pb = {(int)pc[2 * kstep][0], (int)pc[2 * kstep][1], (int)pc[2 * kstep][2], (int)pc[2 * kstep][3],
+              (int)pc[2 * kstep + 1][0], (int)pc[2 * kstep + 1][1], (int)pc[2 * kstep + 1][2], (int)pc[2 * kstep + 1][3]};
+    int pscale = psc[2 * kstep + h];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) {
+      v8i va;
+      // byte t of read q: key 64*kstep + 32*(q/2) + 16*(q%2) + 8*(t/4) + 4*h + t%4, d = 32*dt + lane%32
+      const int t8 = l16 >> 1;
+      const int dcol = dt * 32 + 16 * (g16 & 1) + 8 * (l16 & 1);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        int key = 64 * kstep + 32 * (q >> 1) + 16 * (q & 1) + 8 * (t8 >> 2) + 4 * h + (t8 & 3);
+        v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sV + key * KP + dcol));
+        va[2 * q] = rv[0];
+        va[2 * q + 1] = rv[1];
+      }
+      int vscale = sVs[(2 * kstep + h) * D + dt * 32 + r];
+      st.o[dt] = mfma_mx(va, pb, st.o[dt], vscale, pscale);
+    }
+  }
+}
+
+// Q operand (B of S^T = K Q^T, bf16) for query row `qrow` (zeros if invalid): MFMA kk
+// takes d = 16*kk + 8*h .. +7, dequantized with the row's E8M0 scale of that 32-block.
+template <int D>
+__device__ __forceinline__ void load_q(v4i* qb, const uint8_t* qrow, const uint8_t* qsrow, bool valid, int h) {
+#pragma unroll
+  for (int kk = 0; kk < D / 16; kk++) {
+    v4i o = {0, 0, 0, 0};
+    if (valid) {
+      v2i w = *reinterpret_cast<const v2i*>(qrow + 16 * kk + 8 * h);
+      o = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1], e8m0_as_float(qsrow[kk / 2]));
+    }
+    qb[kk] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill.  Workgroup = 4 waves; wave w handles 32 query positions of one head.
+// The workgroup covers hpw heads of one KV group x qpw positions, so the K/V
+// tile in LDS serves 4 x 32 query rows.  grid = (n_qblk, B * Hkv * group / hpw).
+// ---------------------------------------------------------------------------
+template <int D, bool SOFTCAP>
+__device__ void prefill_impl(const FaArgs& a) {
+  __shared__ __attribute__((aligned(16))) uint8_t sK[2][Lds<D>::TILEK];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[2][Lds<D>::TILE];
+  __shared__ __attribute__((aligned(16))) uint8_t sVs[2][Lds<D>::SC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int qblk = a.causal ? (a.n_qblk - 1 - (int)blockIdx.x) : (int)blockIdx.x;   // longest rows first
+  const int chunks = a.group / a.hpw;
+  const int bk = blockIdx.y / chunks;               // b * Hkv + kvh
+  const int hc = blockIdx.y % chunks;
+  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
+  const int head = kvh * a.group + hc * a.hpw + (wave % a.hpw);
+  const int q0 = qblk * a.qpw;                      // first query row of the workgroup
+  const int qw0 = q0 + (wave / a.hpw) * 32;         // first query row of this wave
+  const int qi = qw0 + r;
+  const bool qvalid = qi < a.Sq;
+  const int qpos = a.q_pos0 + qi;
+
+  const int64_t bh = (int64_t)b * a.Hq + head;
+  v4i qb[D / 16];
+  load_q<D>(qb, a.q + (bh * a.Sq + qi) * D, a.qs + (bh * a.Sq + qi) * (D / 32), qvalid, h);
+
+  // key-block range of the workgroup
+  const int qmax_wg = min(q0 + a.qpw, a.Sq) - 1;
+  const int nkb = (a.Sk + BN - 1) / BN;
+  int j0 = 0, j1 = nkb;
+  if (a.window > 0) j0 = max(0, a.q_pos0 + q0 - a.window + 1) / BN;
+  if (a.causal) j1 = min(nkb, max(0, a.q_pos0 + qmax_wg) / BN + 1);
+  // wave's query-position range (for skipping and mask decisions)
+  const int wq_lo = a.q_pos0 + qw0, wq_hi = a.q_pos0 + min(qw0 + 31, a.Sq - 1);
+  const bool wave_live = qw0 < a.Sq;
+
+  const uint8_t* kb = a.k + (int64_t)bk * a.Sk * D;
+  const uint8_t* ksb = a.ks + (int64_t)bk * a.Sk * (D / 32);
+  const uint8_t* vb = a.v + (int64_t)bk * a.Sk * D;
+  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Sk / 32) * D;
+
+  WaveState<D> st;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; dt++) st.o[dt] = (v16f){};
+  st.m = -INFINITY;
+  st.l = 0.0f;
+
+  BlockRegs<D> regs;
+  if (j0 < j1) {
+    load_block<D>(regs, kb, ksb, vb, vsb, j0 * BN, a.Sk, tid);
+    store_block<D>(regs, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
+  }
+  __syncthreads();
+  for (int j = j0; j < j1; j++) {
+    const int buf = (j - j0) & 1;
+    if (j + 1 < j1) load_block<D>(regs, kb, ksb, vb, vsb, (j + 1) * BN, a.Sk, tid);
+    const int key0 = j * BN, key1 = key0 + BN - 1;
+    bool skip = !wave_live || (a.causal && key0 > wq_hi) || (a.window > 0 && key1 + a.window <= wq_lo);
+    if (!skip) {
+      bool need_mask = (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
+                       (qw0 + 31 >= a.Sq);
+      wave_block<D, SOFTCAP>(st, qb, sK[buf], sV[buf], sVs[buf], key0, qpos, qvalid, need_mask, a, lane);
+    }
+    if (j + 1 < j1) store_block<D>(regs, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
+    __syncthreads();
+  }
+
+  // ---- finalize: O = O / l (0 where no key was visible)
+  float l = st.l + __shfl_xor(st.l, 32);
+  float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if (qvalid) {
+    float* orow = a.o + (bh * a.Sq + qi) * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        float4 w = make_float4(st.o[dt][4 * g] * inv, st.o[dt][4 * g + 1] * inv, st.o[dt][4 * g + 2] * inv,
+                               st.o[dt][4 * g + 3] * inv);
+        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * h) = w;
+      }
+  }
+}
+
+#define MXFA_PREFILL(D, SC, NAME)                                                      \
+  extern "C" __global__ void __launch_bounds__(256) NAME(FaArgs a) { prefill_impl<D, SC>(a); }
+MXFA_PREFILL(64, false, mxfa_prefill_d64)
+MXFA_PREFILL(128, false, mxfa_prefill_d128)
+MXFA_PREFILL(256, false, mxfa_prefill_d256)
+MXFA_PREFILL(64, true, mxfa_prefill_d64_softcap)
+MXFA_PREFILL(128, true, mxfa_prefill_d128_softcap)
+MXFA_PREFILL(256, true, mxfa_prefill_d256_softcap)
+
+// ---------------------------------------------------------------------------
+// Decode (q_len = 1, split-KV).  The keys of each (b, KV head) are cut into
+// nparts chunks of split_len keys; wave w of workgroup x processes chunk
+// part = NW*x + w (NW = 4, or 2 for D = 256) as an independent streaming pass and writes its partial
+// (m, l, O); mxfa_decode_combine merges the partials in part order.  The
+// group's query heads are the wave's query columns (column c = head kvh*group + c).
+// ---------------------------------------------------------------------------
+// Waves per decode workgroup (each wave has private LDS tiles).
+template <int D> struct DecodeWaves { static constexpr int N = D == 256 ? 2 : 4; };
+
+template <int D, bool SOFTCAP>
+__device__ void decode_impl(const FaArgs& a) {
+  constexpr int NW = DecodeWaves<D>::N;
+  __shared__ __attribute__((aligned(16))) uint8_t sK[NW][Lds<D>::TILEK];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[NW][Lds<D>::TILE];
+  __shared__ __attribute__((aligned(16))) uint8_t sVs[NW][Lds<D>::SC];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int part = blockIdx.x * NW + (threadIdx.x >> 6);
+  const int bk = blockIdx.y;
+  if (part >= a.n_qblk) return;                       // waves past the last chunk have no work
+  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
+  const bool qvalid = r < a.group;
+  const int head = kvh * a.group + (qvalid ? r : 0);
+  const int64_t bh = (int64_t)b * a.Hq + head;
+  const int qpos = a.q_pos0;                          // the single query's position
+
+  v4i qb[D / 16];
+  load_q<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
+
+  const uint8_t* kb = a.k + (int64_t)bk * a.Sk * D;
+  const uint8_t* ksb = a.ks + (int64_t)bk * a.Sk * (D / 32);
+  const uint8_t* vb = a.v + (int64_t)bk * a.Sk * D;
+  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Sk / 32) * D;
+
+  const int kbeg = part * a.split_len;
+  const int kend = min(kbeg + a.split_len, a.Sk);
+
+  WaveState<D> st;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; dt++) st.o[dt] = (v16f){};
+  st.m = -INFINITY;
+  st.l = 0.0f;
+
+  // each wave stages its own blocks through its own LDS slot (64 lanes load)
+  constexpr int CPR = D / 16;
+  constexpr int PERW = BN * CPR / 64;
+  constexpr int KP = Lds<D>::KP;
+  constexpr int KPB = Lds<D>::KPB;
+  for (int key0 = kbeg; key0 < kend; key0 += BN) {
+#pragma unroll
+    for (int i = 0; i < PERW; i++) {
+      int c = lane + 64 * i;
+      int row = c / CPR, col = (c % CPR) * 16;
+      int key = key0 + row;
+      v4i zk = {0, 0, 0, 0}, zv = {0, 0, 0, 0};
+      uint32_t ksc = 0;
+      if (key < kend) {
+        zk = *reinterpret_cast<const v4i*>(kb + (int64_t)key * D + col);
+        zv = *reinterpret_cast<const v4i*>(vb + (int64_t)key * D + col);
+        ksc = ksb[(int64_t)key * (D / 32) + col / 32];
+      }
+      if (a.v_e3m2) {
+#pragma unroll
+        for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
+      }
+      float sc = e8m0_as_float(ksc);
+      v4i b0 = fp8x8_to_bf16x8((uint32_t)zk[0], (uint32_t)zk[1], sc);
+      v4i b1 = fp8x8_to_bf16x8((uint32_t)zk[2], (uint32_t)zk[3], sc);
+      *reinterpret_cast<v4i*>(&sK[wave][row * KPB + col * 2]) = b0;
+      *reinterpret_cast<v4i*>(&sK[wave][row * KPB + col * 2 + 16]) = b1;
+      *reinterpret_cast<v4i*>(&sV[wave][row * KP + col]) = zv;
+    }
+    constexpr int SCW = BN * D / 32 / 4;   // V scale dwords per block
+    for (int i = lane; i < SCW; i += 64) {
+      int byte = i * 4;
+      int vk32 = key0 / 32 + byte / D;
+      uint32_t vw = vk32 * 32 < kend ? *reinterpret_cast<const uint32_t*>(vsb + (int64_t)(key0 / 32) * D + byte) : 0u;
+      *reinterpret_cast<uint32_t*>(&sVs[wave][byte]) = vw;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const bool need_mask = true;           // columns >= group are padding and must be masked
+    wave_block<D, SOFTCAP>(st, qb, sK[wave], sV[wave], sVs[wave], key0, qpos, qvalid, need_mask, a, lane);
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // partial outputs (unnormalized O, m in x units, full l)
+  float l = st.l + __shfl_xor(st.l, 32);
+  const int nparts = a.n_qblk;
+  if (qvalid) {
+    float* po = a.part_o + (bh * nparts + part) * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *reinterpret_cast<float4*>(po + dt * 32 + 8 * g + 4 * h) =
+            make_float4(st.o[dt][4 * g], st.o[dt][4 * g + 1], st.o[dt][4 * g + 2], st.o[dt][4 * g + 3]);
+    if (h == 0) {
+      a.part_ml[(bh * nparts + part) * 2] = st.m;
+      a.part_ml[(bh * nparts + part) * 2 + 1] = l;
+    }
+  }
+}
+
+#define MXFA_DECODE(D, SC, NAME)                                                       \
+  extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<D>::N) NAME(FaArgs a) { decode_impl<D, SC>(a); }
+MXFA_DECODE(64, false, mxfa_decode_d64)
+MXFA_DECODE(128, false, mxfa_decode_d128)
+MXFA_DECODE(256, false, mxfa_decode_d256)
+MXFA_DECODE(64, true, mxfa_decode_d64_softcap)
+MXFA_DECODE(128, true, mxfa_decode_d128_softcap)
+MXFA_DECODE(256, true, mxfa_decode_d256_softcap)
+
+// Merge nparts partials per (b, query head) in part order: O = sum_i O_i 2^{(m_i - M) c} / sum_i l_i 2^{(m_i - M) c}.
+// One workgroup of D threads per query head.
+extern "C" __global__ void __launch_bounds__(256) mxfa_decode_combine(FaArgs a) {
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const int D = blockDim.x;
+  const int nparts = a.n_qblk;
+  const float c = a.cap_log2 > 0.0f ? 1.0f : a.c_log2;
+  const float* ml = a.part_ml + bh * nparts * 2;
+  float M = -INFINITY;
+  for (int i = 0; i < nparts; i++)
+    if (ml[2 * i + 1] > 0.0f) M = fmaxf(M, ml[2 * i]);
+  float L = 0.0f, acc = 0.0f;
+  if (M != -INFINITY) {
+    const float mc = M * c;
+    for (int i = 0; i < nparts; i++) {
+      float li = ml[2 * i + 1];
+      if (!(li > 0.0f)) continue;
+      float w = __builtin_amdgcn_exp2f(__builtin_fmaf(ml[2 * i], c, -mc));
+      L += li * w;
+      acc += a.part_o[(bh * nparts + i) * D + d] * w;
+    }
+  }
+  a.o[bh * D + d] = L > 0.0f ? acc / L : 0.0f;
+}

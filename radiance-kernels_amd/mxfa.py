@@ -1,0 +1,199 @@
+"""Python host mirror of the libmxfa C ABI (include/mxfa.h).
+
+The reference exposes its MXFP8 flash-attention operator as generated headers plus a
+bare-metal entry point (kernels/flash_attention_mx_gqa/fa_gen_data.py:119-159,
+kernel.cpp:91-191); its Python side (flash_attention_model.py) names the operations
+make_inputs / mx_quantize_cols / mx_attention_flash*.  This module keeps that
+vocabulary on top of the C ABI:
+
+    fill_normal       -> make_inputs / make_inputs_gqa (synthetic N(0,1) [+ outliers])
+    quantize_rows     -> mx_quantize_cols on Q and K (32-blocks along D)
+    quantize_cols     -> mx_quantize_cols(V.t()) (32-blocks along the key axis)
+    prefill           -> mx_attention_flash[_causal_gqa | _gemma]
+    decode            -> the same recurrence over an MXFP8 KV cache (split-KV)
+    requant_p         -> the P requant step of fused_softmax_requant
+
+torch is used only to hold device memory and name the stream; every call goes through
+ctypes into libmxfa.so, which launches gfx950 kernels.  There is no fallback: if the
+library or the code object is missing, calls raise.
+"""
+import ctypes
+import math
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmxfa.so")
+
+FMT_E4M3 = 0
+FMT_E3M2 = 1
+DEFAULT_BLOCK_N = 64
+
+STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "HIP error", 4: "code object error",
+          5: "workspace too small"}
+
+
+class MxfaError(RuntimeError):
+    def __init__(self, status, detail):
+        self.status = status
+        super().__init__(f"mxfa: {STATUS.get(status, status)}: {detail}")
+
+
+class AttnParams(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+        ("seq_q", ctypes.c_int32), ("seq_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("causal", ctypes.c_int32), ("q_pos0", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("v_fmt", ctypes.c_int32),
+        ("block_n", ctypes.c_int32),
+    ]
+
+
+def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0,
+                v_fmt=FMT_E4M3, block_n=0):
+    return AttnParams(B, Hq, Hkv, Sq, Sk, D, int(bool(causal)), int(q_pos0), int(window),
+                      float(scale if scale is not None else 1.0 / math.sqrt(D)), float(softcap), int(v_fmt),
+                      int(block_n))
+
+
+EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
+           "mxfa_requant_p", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
+           "mxfa_last_error", "mxfa_version")
+
+_lib = None
+
+
+def lib():
+    """Load libmxfa.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MxfaError(4, f"{LIB_PATH} not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u8p, f32p = ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p
+        P = ctypes.POINTER
+        L.mxfa_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int, u8p, u8p, vp]
+        L.mxfa_quantize_cols.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int, u8p, u8p, vp]
+        L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
+        L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
+        L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
+        L.mxfa_requant_p.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, u8p, u8p, vp]
+        L.mxfa_fill_normal.argtypes = [f32p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp]
+        L.mxfa_status_string.argtypes = [ctypes.c_int]
+        L.mxfa_status_string.restype = ctypes.c_char_p
+        L.mxfa_last_error.restype = ctypes.c_char_p
+        L.mxfa_version.restype = ctypes.c_int32
+        for name in ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
+                     "mxfa_requant_p", "mxfa_fill_normal", "mxfa_init"):
+            getattr(L, name).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _check(st):
+    if st != 0:
+        raise MxfaError(st, lib().mxfa_last_error().decode())
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(stream if isinstance(stream, int) else stream.cuda_stream)
+
+
+def init():
+    _check(lib().mxfa_init())
+
+
+def quantize_rows(x, fmt=FMT_E4M3, stream=None):
+    """x: contiguous float32 CUDA tensor [..., cols] -> (codes uint8 [..., cols], scales uint8 [..., cols/32])."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty(tuple(x.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=x.device)
+    _check(lib().mxfa_quantize_rows(_ptr(x), rows, cols, fmt, _ptr(codes), _ptr(scales), _stream(stream)))
+    return codes, scales
+
+
+def quantize_cols(x, fmt=FMT_E4M3, stream=None):
+    """x: contiguous float32 CUDA tensor [..., rows, cols]; 32-blocks along rows ->
+    (codes [..., rows, cols], scales [..., rows/32, cols])."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    rows, cols = x.shape[-2], x.shape[-1]
+    mats = x.numel() // (rows * cols)
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty(tuple(x.shape[:-2]) + (rows // 32, cols), dtype=torch.uint8, device=x.device)
+    _check(lib().mxfa_quantize_cols(_ptr(x), mats, rows, cols, fmt, _ptr(codes), _ptr(scales), _stream(stream)))
+    return codes, scales
+
+
+def requant_p(p, stream=None):
+    import torch
+    assert p.is_cuda and p.dtype == torch.float32 and p.is_contiguous()
+    cols = p.shape[-1]
+    rows = p.numel() // cols
+    codes = torch.empty(p.shape, dtype=torch.uint8, device=p.device)
+    scales = torch.empty(tuple(p.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=p.device)
+    _check(lib().mxfa_requant_p(_ptr(p), rows, cols, _ptr(codes), _ptr(scales), _stream(stream)))
+    return codes, scales
+
+
+def fill_normal(x, seed, outlier_p=0.0, outlier_mul=20.0, stream=None):
+    """Fill a contiguous float32 CUDA tensor with N(0,1) values (+ outliers) in place."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    _check(lib().mxfa_fill_normal(_ptr(x), x.numel(), ctypes.c_uint64(seed & (2 ** 64 - 1)), float(outlier_p),
+                                  float(outlier_mul), _stream(stream)))
+    return x
+
+
+def prefill(p, q, qs, k, ks, v, vs, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device=q.device)
+    _check(lib().mxfa_prefill(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
+                              _stream(stream)))
+    return out
+
+
+def decode_plan(p):
+    sl = ctypes.c_int32(0)
+    ws = ctypes.c_size_t(0)
+    _check(lib().mxfa_decode_plan(ctypes.byref(p), ctypes.byref(sl), ctypes.byref(ws)))
+    return sl.value, ws.value
+
+
+def decode(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):
+    import torch
+    _, ws_bytes = decode_plan(p)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty((p.batch, p.num_q_heads, 1, p.head_dim), dtype=torch.float32, device=q.device)
+    _check(lib().mxfa_decode(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
+                             _ptr(workspace), workspace.numel(), _stream(stream)))
+    return out
+
+
+def attention_flops(p):
+    """Algorithmic FLOP of one call: 4*D per visible (query, key) pair (QK^T + PV)."""
+    return 4.0 * p.head_dim * p.batch * p.num_q_heads * visible_pairs(p)
+
+
+def visible_pairs(p):
+    """Visible (query, key) pairs of one head under the causal / window mask."""
+    total = 0
+    for i in range(p.seq_q):
+        qpos = p.q_pos0 + i
+        hi = min(p.seq_k - 1, qpos) if p.causal else p.seq_k - 1
+        lo = max(0, qpos - p.window + 1) if p.window > 0 else 0
+        if hi >= lo:
+            total += hi - lo + 1
+    return total

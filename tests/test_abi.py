@@ -1,0 +1,100 @@
+"""CPU tests of the C ABI: the library loads, exports every entry point declared in
+include/mxfa.h, and rejects invalid arguments before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import mxfa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    src = open(os.path.join(ROOT, "include", "mxfa.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mxfa_[a-z_0-9]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = mxfa.lib()
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(mxfa.EXPORTS) <= set(names)
+
+
+def test_code_object_present_and_for_gfx950():
+    path = os.path.join(os.path.dirname(mxfa.LIB_PATH), "mxfa_kernels.hsaco")
+    data = open(path, "rb").read()
+    assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    assert b"gfx950" in data
+    for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_requant_p_rows"):
+        assert k.encode() in data
+
+
+def test_version_and_status_strings():
+    L = mxfa.lib()
+    assert L.mxfa_version() == 1
+    assert L.mxfa_status_string(0) == b"ok"
+    assert L.mxfa_status_string(5) == b"workspace too small"
+
+
+def _call_prefill(p):
+    L = mxfa.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    ptr = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
+    return L.mxfa_prefill(ctypes.byref(p), ptr, ptr, ptr, ptr, ptr, ptr, ptr, None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(Hq=3, Hkv=2), 1),              # Hq % Hkv
+    (dict(D=48), 1),                     # D % 32
+    (dict(D=96), 2),                     # unsupported head dim
+    (dict(Sk=100), 1),                   # Sk % 32
+    (dict(B=0), 1),
+    (dict(window=-1), 1),
+    (dict(softcap=-1.0), 1),
+    (dict(block_n=128), 2),
+])
+def test_prefill_argument_validation(kw, status):
+    a = dict(B=1, Hq=2, Hkv=2, Sq=32, Sk=64, D=64, window=0, softcap=0.0, block_n=0)
+    a.update(kw)
+    p = mxfa.make_params(a["B"], a["Hq"], a["Hkv"], a["Sq"], a["Sk"], a["D"], window=a["window"],
+                         softcap=a["softcap"], block_n=a["block_n"])
+    assert _call_prefill(p) == status
+    assert mxfa.lib().mxfa_last_error()
+
+
+def test_null_and_misaligned_pointers_rejected():
+    L = mxfa.lib()
+    p = mxfa.make_params(1, 1, 1, 32, 64, 64)
+    assert L.mxfa_prefill(ctypes.byref(p), None, None, None, None, None, None, None, None) == 1
+    buf = (ctypes.c_uint8 * 64)()
+    base = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
+    mis = ctypes.c_void_p(base + 1)
+    assert L.mxfa_prefill(ctypes.byref(p), mis, mis, mis, mis, mis, mis, mis, None) == 1
+
+
+def test_decode_validation_and_plan():
+    L = mxfa.lib()
+    p = mxfa.make_params(64, 32, 8, 1, 8192, 128, causal=True, q_pos0=8191)
+    sl, ws = mxfa.decode_plan(p)
+    assert sl % 64 == 0 and sl >= 64
+    nparts = -(-8192 // sl)
+    assert ws >= 64 * 32 * nparts * (128 + 2) * 4
+    p2 = mxfa.make_params(1, 1, 1, 2, 64, 64)
+    sl_ = ctypes.c_int32(0)
+    ws_ = ctypes.c_size_t(0)
+    assert L.mxfa_decode_plan(ctypes.byref(p2), ctypes.byref(sl_), ctypes.byref(ws_)) == 1
+
+
+def test_quantize_argument_validation():
+    L = mxfa.lib()
+    assert L.mxfa_quantize_rows(None, 4, 48, 0, None, None, None) == 1
+    assert L.mxfa_quantize_rows(None, 0, 64, 0, None, None, None) == 0     # empty input: no-op
+    assert L.mxfa_quantize_cols(None, 1, 48, 64, 0, None, None, None) == 1
+    assert L.mxfa_quantize_cols(None, 0, 64, 64, 0, None, None, None) == 0
+    assert L.mxfa_requant_p(None, 4, 33, None, None, None) == 1

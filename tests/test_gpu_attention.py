@@ -1,0 +1,147 @@
+"""GPU parity of MXFP8 prefill and decode against the oracle (same block size and
+split schedule), to the north_star tolerance: rel-L2 <= 5e-3 and max-abs <= 2e-2.
+Operands are generated and quantized on the GPU; the oracle first re-quantizes the
+same fp32 values and must reproduce the codes bit for bit."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import mxfa  # noqa: E402
+import oracle as O  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, gen_qkv, np_, oracle_params  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.0, v_fmt=mxfa.FMT_E4M3,
+             seed=0, outlier_p=0.0, q_mul=1.0, heads=None, check_codes=True):
+    print(f"case B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Sk{Sk} D{D} causal{causal} q_pos0 {q_pos0} window {window} "
+          f"softcap {softcap} v_fmt {v_fmt} seed {seed}", flush=True)
+    fp, dev, host = gen_qkv(B, Hq, Hkv, Sq, Sk, D, seed, outlier_p=outlier_p, q_mul=q_mul, v_fmt=v_fmt)
+    if check_codes:
+        oq, oqs = O.quantize_rows(np_(fp["Q"]), O.FMT_E4M3)
+        np.testing.assert_array_equal(host["q"], oq)
+        np.testing.assert_array_equal(host["qs"], oqs)
+        ov, ovs = O.quantize_cols(np_(fp["V"]), v_fmt)
+        np.testing.assert_array_equal(host["v"], ov)
+        np.testing.assert_array_equal(host["vs"], ovs)
+    p = mxfa.make_params(B, Hq, Hkv, Sq, Sk, D, causal=causal, q_pos0=q_pos0, window=window, softcap=softcap,
+                         v_fmt=v_fmt)
+    out = torch.full((B, Hq, Sq, D), float("nan"), dtype=torch.float32, device=DEV)
+    mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
+    torch.cuda.synchronize()
+    o = np_(out)
+    assert np.all(np.isfinite(o)), "coverage: some O elements were not written"
+    want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
+                       block_n=mxfa.DEFAULT_BLOCK_N, heads=heads)
+    if heads is not None:
+        idx = np.array(heads)
+        o = o.reshape(B * Hq, Sq, D)[idx]
+        want = want.reshape(B * Hq, Sq, D)[idx]
+    rel, mab = errors(o, want)
+    print(f"   rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+    return p, dev, out
+
+
+def test_config1_single_head_noncausal():
+    """B=1 H=1 S=256 D=64, non-causal."""
+    run_case(1, 1, 1, 256, 256, 64, seed=1)
+
+
+def test_reference_gqa_tile():
+    """The reference GQA kernel's own case: NQ=8, NKV=2, Sq=64, Sk=256, d=64, q_pos0=64
+    (kernels/regen_data.sh:31-34)."""
+    run_case(1, 8, 2, 64, 256, 64, causal=True, q_pos0=64, seed=2)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_causal_gqa_head_dims(D):
+    run_case(2, 8, 2, 160, 160, D, causal=True, seed=3 + D)
+
+
+def test_ragged_lengths():
+    """Sq not a multiple of the 32-row wave tile; Sk not a multiple of the 64-key block."""
+    run_case(1, 4, 4, 77, 96, 128, causal=False, seed=5)
+    run_case(2, 4, 1, 45, 224, 128, causal=True, q_pos0=179, seed=6)
+
+
+def test_gemma_softcap_window_e3m2():
+    """Reference gemma variant semantics: softcap before max, sliding window, V in E3M2."""
+    run_case(1, 4, 2, 384, 384, 256, causal=True, window=128, softcap=50.0, v_fmt=mxfa.FMT_E3M2, seed=7)
+
+
+def test_softcap_saturated_queries():
+    """The reference's softcap stress: queries x50 so the cap saturates."""
+    run_case(1, 2, 1, 128, 128, 128, causal=True, softcap=50.0, q_mul=50.0, seed=8)
+
+
+def test_outliers():
+    """1% of elements x20, as in the S=4096 GQA headline config."""
+    run_case(1, 8, 2, 256, 256, 128, causal=True, outlier_p=0.01, seed=9)
+
+
+def test_fully_masked_rows_are_zero():
+    B, H, Sq, Sk, D = 1, 2, 32, 64, 64
+    p, dev, out = run_case(B, H, H, Sq, Sk, D, causal=True, q_pos0=200, window=100, seed=10)
+    assert np.all(np_(out) == 0.0)
+
+
+def test_deterministic():
+    p, dev, out = run_case(1, 4, 2, 256, 256, 128, causal=True, seed=11)
+    out2 = mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
+def test_baseline_configs_sampled_heads(cfg):
+    """Full BASELINE shapes; all heads computed on the GPU (coverage + finiteness),
+    a sample of heads compared with the oracle."""
+    if cfg == "c2":
+        run_case(4, 16, 16, 2048, 2048, 128, causal=True, seed=21, heads=[0, 37], check_codes=False)
+    elif cfg == "c3":
+        run_case(2, 32, 8, 4096, 4096, 128, causal=True, outlier_p=0.01, seed=22, heads=[5, 63], check_codes=False)
+    else:
+        run_case(1, 16, 8, 8192, 8192, 256, causal=True, window=4096, softcap=50.0, v_fmt=mxfa.FMT_E3M2, seed=23,
+                 heads=[3], check_codes=False)
+
+
+def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=0.0):
+    print(f"decode B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} seed {seed}", flush=True)
+    fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L, D, seed, v_fmt=v_fmt)
+    p = mxfa.make_params(B, Hq, Hkv, 1, L, D, causal=True, q_pos0=L - 1, softcap=softcap, v_fmt=v_fmt)
+    split_len, _ = mxfa.decode_plan(p)
+    out = torch.full((B, Hq, 1, D), float("nan"), dtype=torch.float32, device=DEV)
+    mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
+    torch.cuda.synchronize()
+    o = np_(out)
+    assert np.all(np.isfinite(o))
+    want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
+                       block_n=mxfa.DEFAULT_BLOCK_N, split_len=split_len, heads=heads)
+    if heads is not None:
+        idx = np.array(heads)
+        o = o.reshape(B * Hq, D)[idx]
+        want = want.reshape(B * Hq, D)[idx]
+    rel, mab = errors(o, want)
+    print(f"   split_len {split_len} rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+    return p, dev, out
+
+
+def test_decode_small():
+    run_decode(4, 32, 8, 1024, 128, seed=30)
+
+
+def test_decode_ragged_and_e3m2():
+    run_decode(3, 8, 2, 480, 64, seed=31, v_fmt=mxfa.FMT_E3M2)
+    run_decode(2, 16, 8, 2080, 256, seed=32, softcap=30.0)
+
+
+def test_decode_config5_sampled():
+    """B=64, Hq=32, Hkv=8, D=128, KV length 8192."""
+    p, dev, out = run_decode(64, 32, 8, 8192, 128, seed=33, heads=[0, 1000, 2047])
+    out2 = mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
