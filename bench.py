@@ -1,0 +1,161 @@
+"""Benchmark: MXFP8 flash attention on one MI355X.
+
+Headline (BASELINE.json metric "MXFP8 attn TFLOP/s + % MFMA peak (S=4096 GQA); decode
+KV GB/s, 1 GPU"): a step is one mxfa_prefill call over configs[2] -- B=2, Hq=32,
+Hkv=8, S=4096, D=128, causal, E4M3 block-32 MX operands with 1% of elements x20.
+Operands are generated and quantized on the GPU before timing and stay resident in
+HBM.  value = algorithmic TFLOP/s (4*D FLOP per visible (query, key) pair).  The
+decode config is timed the same way and reported as HBM GB/s.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+
+Prints one JSON line.  Only --gpus 1 is supported (this path runs on one GPU).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "radiance-kernels_amd"))
+
+MXFP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 / MXFP8 MFMA
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+
+
+def prefill_config():
+    return dict(B=2, Hq=32, Hkv=8, S=4096, D=128, causal=True, outlier_p=0.01)
+
+
+def decode_config():
+    return dict(B=64, Hq=32, Hkv=8, L=8192, D=128)
+
+
+def make_prefill(torch, mxfa, c, seed=1):
+    dev = "cuda:0"
+    Q = torch.empty((c["B"], c["Hq"], c["S"], c["D"]), dtype=torch.float32, device=dev)
+    K = torch.empty((c["B"], c["Hkv"], c["S"], c["D"]), dtype=torch.float32, device=dev)
+    V = torch.empty_like(K)
+    for i, X in enumerate((Q, K, V)):
+        mxfa.fill_normal(X, seed * 3 + i, c["outlier_p"], 20.0)
+    q, qs = mxfa.quantize_rows(Q)
+    k, ks = mxfa.quantize_rows(K)
+    v, vs = mxfa.quantize_cols(V)
+    del Q, K, V
+    p = mxfa.make_params(c["B"], c["Hq"], c["Hkv"], c["S"], c["S"], c["D"], causal=c["causal"])
+    return p, (q, qs, k, ks, v, vs)
+
+
+def time_calls(torch, fn, steps, warmup):
+    """Average ms per call with HIP events on the launch stream (torch's current stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        fn()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
+
+
+def cpu_baseline(mxfa, p, ops_host, threads):
+    """The CPU oracle (this repo's C restatement, threaded) on a bounded sample of the
+    same workload: batch 0, query heads 0-3 (one KV group) = 1/16 of configs[2]."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    op = O.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim,
+                       causal=bool(p.causal), scale=p.softmax_scale)
+    heads = [0, 1, 2, 3]
+    t0 = time.time()
+    O.attention(op, *ops_host, block_n=mxfa.DEFAULT_BLOCK_N, heads=heads, nthreads=threads)
+    dt = time.time() - t0
+    flops = 4.0 * p.head_dim * len(heads) * mxfa.visible_pairs(p)
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"batch 0, query heads 0-3 of configs[2] ({flops / 1e9:.1f} GFLOP, {dt:.2f} s wall)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this path runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mxfa
+    torch.cuda.set_device(0)
+    mxfa.init()
+
+    c = prefill_config()
+    p, ops = make_prefill(torch, mxfa, c)
+    out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device="cuda:0")
+    ms = time_calls(torch, lambda: mxfa.prefill(p, *ops, out=out), args.steps, args.warmup)
+    flops = mxfa.attention_flops(p)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    result = {
+        "metric": "MXFP8 attn TFLOP/s + % MFMA peak (S=4096 GQA); decode KV GB/s, 1 GPU",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp8-e4m3 (QK^T on bf16 MFMA from exact dequant, PV on scaled MXFP8 MFMA, fp32 softmax/accum)",
+        "data": "synthetic: N(0,1) with 1% of elements x20, generated and MX-quantized on the GPU (mxfa_fill_normal, mxfa_quantize_*)",
+        "config": {"workload": "configs[2]: MXFP8 GQA causal prefill B=2 Hq=32 Hkv=8 S=4096 D=128",
+                   "batch": c["B"], "q_heads": c["Hq"], "kv_heads": c["Hkv"], "seq": c["S"], "head_dim": c["D"],
+                   "causal": True, "block_n": mxfa.DEFAULT_BLOCK_N, "gflop_per_step": round(flops / 1e9, 2)},
+        "pct_mxfp8_peak": round(100.0 * tflops / MXFP8_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": None},
+    }
+
+    if not args.no_decode:
+        dc = decode_config()
+        dev = "cuda:0"
+        Qd = torch.empty((dc["B"], dc["Hq"], 1, dc["D"]), dtype=torch.float32, device=dev)
+        Kd = torch.empty((dc["B"], dc["Hkv"], dc["L"], dc["D"]), dtype=torch.float32, device=dev)
+        mxfa.fill_normal(Qd, 11)
+        mxfa.fill_normal(Kd, 12)
+        qd, qsd = mxfa.quantize_rows(Qd)
+        kd, ksd = mxfa.quantize_rows(Kd)
+        mxfa.fill_normal(Kd, 13)
+        vd, vsd = mxfa.quantize_cols(Kd)
+        del Kd
+        pd = mxfa.make_params(dc["B"], dc["Hq"], dc["Hkv"], 1, dc["L"], dc["D"], causal=True, q_pos0=dc["L"] - 1)
+        _, ws_bytes = mxfa.decode_plan(pd)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        od = torch.empty((dc["B"], dc["Hq"], 1, dc["D"]), dtype=torch.float32, device=dev)
+        msd = time_calls(torch, lambda: mxfa.decode(pd, qd, qsd, kd, ksd, vd, vsd, out=od, workspace=ws),
+                         args.steps * 5, args.warmup)
+        nbytes = sum(t.numel() for t in (qd, qsd, kd, ksd, vd, vsd)) + od.numel() * 4
+        gbs = nbytes / (msd * 1e-3) / 1e9
+        result["decode"] = {"workload": "configs[4]: decode B=64 Hq=32 Hkv=8 D=128 KV length 8192, E4M3 MX KV cache",
+                            "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(msd, 4),
+                            "bytes_per_call": nbytes, "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        host = [t.cpu().numpy() for t in ops]
+        result["cpu_baseline"] = cpu_baseline(mxfa, p, host, threads)
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
