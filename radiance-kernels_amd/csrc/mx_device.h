@@ -37,10 +37,32 @@ __device__ __forceinline__ int floor_log2f(float x) {
   return (int)E - 127 + (m >= c_log2_thr[E] ? 1 : 0);
 }
 
+// floorf(log2f(x)) for finite x > 0 without a memory table: for a normal x with
+// exponent e the result is e + 1 when the mantissa reaches 2^23 - delta, where
+// delta depends only on the binade of u = (e >= 0 ? e : -e - 1) (log2f rounds to
+// the float grid around the integer e + 1); subnormals use the table.
+__device__ __forceinline__ int floor_log2f_alu(float x) {
+  uint32_t b = __float_as_uint(x) & 0x7fffffffu;
+  int e = (int)(b >> 23) - 127;
+  if (e == -127) return floor_log2f(x);
+  uint32_t u = e >= 0 ? (uint32_t)e : (uint32_t)(-e - 1);
+  int k = 31 - __clz(u | 1u);
+  uint32_t delta = (uint32_t)((0x2C160B05020100ull >> (8 * k)) & 0xffu);
+  uint32_t thr = u < 2u ? 0x800000u : 0x800000u - delta;
+  return e + ((b & 0x7fffffu) >= thr ? 1 : 0);
+}
+
 // E8M0 block scale code; amax = max |x| over the block (NaN already dropped by fmaxf).
 __device__ __forceinline__ uint32_t scale_code(float amax, int log2_pmax) {
   if (!(amax > 0.0f) || __builtin_isinf(amax)) return 0u;
   int s2 = floor_log2f(amax) - log2_pmax + 127;
+  return (uint32_t)(s2 < 0 ? 0 : (s2 > 254 ? 254 : s2));
+}
+
+// Same rule without the memory table (the attention kernels' P blocks).
+__device__ __forceinline__ uint32_t scale_code_alu(float amax, int log2_pmax) {
+  if (!(amax > 0.0f) || __builtin_isinf(amax)) return 0u;
+  int s2 = floor_log2f_alu(amax) - log2_pmax + 127;
   return (uint32_t)(s2 < 0 ? 0 : (s2 > 254 ? 254 : s2));
 }
 

@@ -153,7 +153,7 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_requant_p_rows(const floa
   a = fmaxf(a, __shfl_xor(a, 1));
   a = fmaxf(a, __shfl_xor(a, 2));
   a = fmaxf(a, __shfl_xor(a, 4));
-  uint32_t sc = scale_code(a, 8);
+  uint32_t sc = scale_code_alu(a, 8);
   reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = r1_pack4(v.x, v.y, v.z, v.w, 127 - (int)sc);
   if (part == 0) scales[blk] = (uint8_t)sc;
 }
@@ -194,6 +194,18 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_fill_normal_f32(float* x,
 
 constexpr int BN = 64;          // online-softmax key block (the reference's Bk)
 constexpr int NWAVE = 4;
+
+// Combine a value across the lane pair (l, l ^ 32) with v_permlane32_swap (no LDS):
+// swap(x, x) returns (x of lanes 0-31 | x of lanes 0-31 moved up, x of lanes 32-63 moved
+// down | x of lanes 32-63), so both halves hold their own and their partner's value.
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ v16f mfma_mx(v8i a, v8i b, v16f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
@@ -360,32 +372,36 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   float rmax = -INFINITY;
 #pragma unroll
   for (int t = 0; t < NT; t++) {
-    bmax[t] = fmaxf(tmax[t], __shfl_xor(tmax[t], 32));
+    bmax[t] = pair_max(tmax[t]);
     rmax = fmaxf(rmax, bmax[t]);
   }
-  // P = exp2((x - m) * c): the row maximum gets exactly exp2(0) = 1, like the
-  // reference's exp(S - m); a fused x*c - m*c would leave a rounding residue there
-  // that can move the block's power-of-two scale.
+  // The row maximum must give a block amax of exactly exp2(0) = 1, like the reference's
+  // exp(S - m): a fused x*c - m*c would leave a rounding residue that can move that
+  // block's power-of-two scale, so the amax below uses (max - m) * c.
   const float c = SOFTCAP ? 1.0f : a.c_log2;
   float m_new = fmaxf(st.m, rmax);
   float mu = m_new == -INFINITY ? 0.0f : m_new;
   float corr = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((st.m - mu) * c);
   st.m = m_new;
 
-  // ---- P and the per-tile amax from the tile max (subtract, scale and exp2 are monotone)
+  // ---- P = exp2(fma(x, c, -m*c)); the per-tile amax is exp2((tile max - m) * c), exactly
+  // 1 in the tile holding the row max.  fma and exp2 are monotone, so the amax bounds every
+  // P of the tile; a P at the row max may exceed it by one rounding residue (< 2^-16),
+  // which leaves its code unchanged.
+  const float mcn = -(mu * c);
   float lsum = 0.0f;
   uint32_t pc[NT][4];
   int psc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     float amax = __builtin_amdgcn_exp2f((bmax[t] - mu) * c);
-    uint32_t sc = scale_code(amax, 8);
+    uint32_t sc = scale_code_alu(amax, 8);
     int sh = 127 - (int)sc;
     psc[t] = (int)sc;
     float p[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      p[i] = __builtin_amdgcn_exp2f((s[t][i] - mu) * c);
+      p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], c, mcn));
       lsum += p[i];
     }
 #pragma unroll
@@ -393,11 +409,14 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   }
   st.l = st.l * corr + lsum;
 
-  // ---- O^T = O^T * corr + V^T P^T
+  // ---- O^T = O^T * corr + V^T P^T (the rescale is skipped when no query of the wave
+  // raised its max: corr == 1 exactly and the product would be the identity)
+  if (__any(corr != 1.0f)) {
 #pragma unroll
-  for (int dt = 0; dt < D / 32; dt++)
+    for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
-    for (int i = 0; i < 16; i++) st.o[dt][i] *= corr;
+      for (int i = 0; i < 16; i++) st.o[dt][i] *= corr;
+  }
 
   const int l16 = lane & 15, g16 = lane >> 4;
 #pragma unroll
@@ -452,10 +471,18 @@ __device__ void prefill_impl(const FaArgs& a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, h = lane >> 5;
-  const int qblk = a.causal ? (a.n_qblk - 1 - (int)blockIdx.x) : (int)blockIdx.x;   // longest rows first
+  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
+  // renumber them so that each XCD receives a contiguous range of work items, i.e.
+  // all query blocks of the same KV head land on one XCD and share its L2.
+  const int nwg = (int)(gridDim.x * gridDim.y);
+  const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+  const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
+  const int item = xcd * per + min(xcd, rem) + (lin >> 3);
+  const int qx = item % a.n_qblk, qy = item / a.n_qblk;
+  const int qblk = a.causal ? (a.n_qblk - 1 - qx) : qx;   // longest rows first
   const int chunks = a.group / a.hpw;
-  const int bk = blockIdx.y / chunks;               // b * Hkv + kvh
-  const int hc = blockIdx.y % chunks;
+  const int bk = qy / chunks;                        // b * Hkv + kvh
+  const int hc = qy % chunks;
   const int b = bk / a.Hkv, kvh = bk % a.Hkv;
   const int head = kvh * a.group + hc * a.hpw + (wave % a.hpw);
   const int q0 = qblk * a.qpw;                      // first query row of the workgroup
@@ -489,15 +516,7 @@ __device__ void prefill_impl(const FaArgs& a) {
   st.m = -INFINITY;
   st.l = 0.0f;
 
-  BlockRegs<D> regs;
-  if (j0 < j1) {
-    load_block<D>(regs, kb, ksb, vb, vsb, j0 * BN, a.Sk, tid);
-    store_block<D>(regs, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
-  }
-  __syncthreads();
-  for (int j = j0; j < j1; j++) {
-    const int buf = (j - j0) & 1;
-    if (j + 1 < j1) load_block<D>(regs, kb, ksb, vb, vsb, (j + 1) * BN, a.Sk, tid);
+  auto compute = [&](int j, int buf) {
     const int key0 = j * BN, key1 = key0 + BN - 1;
     bool skip = !wave_live || (a.causal && key0 > wq_hi) || (a.window > 0 && key1 + a.window <= wq_lo);
     if (!skip) {
@@ -505,12 +524,45 @@ __device__ void prefill_impl(const FaArgs& a) {
                        (qw0 + 31 >= a.Sq);
       wave_block<D, SOFTCAP>(st, qb, sK[buf], sV[buf], sVs[buf], key0, qpos, qvalid, need_mask, a, lane);
     }
-    if (j + 1 < j1) store_block<D>(regs, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
+  };
+  if constexpr (D <= 128) {
+    // Two register stages: block j+1 is loaded during iteration j-1 and stored to LDS at
+    // the end of iteration j, so each global load has a whole iteration to land.
+    BlockRegs<D> ra, rb;
+    if (j0 < j1) load_block<D>(ra, kb, ksb, vb, vsb, j0 * BN, a.Sk, tid);
+    if (j0 + 1 < j1) load_block<D>(rb, kb, ksb, vb, vsb, (j0 + 1) * BN, a.Sk, tid);
+    if (j0 < j1) store_block<D>(ra, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
     __syncthreads();
+    auto step = [&](int j, BlockRegs<D>& nxt2, const BlockRegs<D>& nxt1) {
+      const int buf = (j - j0) & 1;
+      if (j + 2 < j1) load_block<D>(nxt2, kb, ksb, vb, vsb, (j + 2) * BN, a.Sk, tid);
+      compute(j, buf);
+      if (j + 1 < j1) store_block<D>(nxt1, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
+      __syncthreads();
+    };
+    for (int j = j0; j < j1; j += 2) {
+      step(j, ra, rb);                // ra was stored last step: refill it with j+2; rb holds j+1
+      if (j + 1 < j1) step(j + 1, rb, ra);
+    }
+  } else {
+    // One register stage (register budget of D = 256): block j+1 loads during block j.
+    BlockRegs<D> regs;
+    if (j0 < j1) {
+      load_block<D>(regs, kb, ksb, vb, vsb, j0 * BN, a.Sk, tid);
+      store_block<D>(regs, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
+    }
+    __syncthreads();
+    for (int j = j0; j < j1; j++) {
+      const int buf = (j - j0) & 1;
+      if (j + 1 < j1) load_block<D>(regs, kb, ksb, vb, vsb, (j + 1) * BN, a.Sk, tid);
+      compute(j, buf);
+      if (j + 1 < j1) store_block<D>(regs, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
+      __syncthreads();
+    }
   }
 
   // ---- finalize: O = O / l (0 where no key was visible)
-  float l = st.l + __shfl_xor(st.l, 32);
+  float l = pair_sum(st.l);
   float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (qvalid) {
     float* orow = a.o + (bh * a.Sq + qi) * D;
@@ -526,7 +578,7 @@ __device__ void prefill_impl(const FaArgs& a) {
 }
 
 #define MXFA_PREFILL(D, SC, NAME)                                                      \
-  extern "C" __global__ void __launch_bounds__(256) NAME(FaArgs a) { prefill_impl<D, SC>(a); }
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { prefill_impl<D, SC>(a); }
 MXFA_PREFILL(64, false, mxfa_prefill_d64)
 MXFA_PREFILL(128, false, mxfa_prefill_d128)
 MXFA_PREFILL(256, false, mxfa_prefill_d256)
@@ -622,7 +674,7 @@ __device__ void decode_impl(const FaArgs& a) {
   }
 
   // partial outputs (unnormalized O, m in x units, full l)
-  float l = st.l + __shfl_xor(st.l, 32);
+  float l = pair_sum(st.l);
   const int nparts = a.n_qblk;
   if (qvalid) {
     float* po = a.part_o + (bh * nparts + part) * D;
