@@ -66,6 +66,21 @@ __device__ __forceinline__ uint32_t scale_code_alu(float amax, int log2_pmax) {
   return (uint32_t)(s2 < 0 ? 0 : (s2 > 254 ? 254 : s2));
 }
 
+// E4M3 block scale code of a finite amax >= 0 (the P blocks), without branches:
+// an amax below 2^-119 (zero and subnormals included) has floor(log2f) - 8 + 127 < 0,
+// i.e. code 0, so the subnormal table is never needed; finite amax stays below the
+// 254 clamp.
+__device__ __forceinline__ uint32_t scale_code_p(float amax) {
+  uint32_t b = __float_as_uint(amax);
+  int e = (int)(b >> 23) - 127;
+  uint32_t u = (uint32_t)(e ^ (e >> 31));            // e >= 0 ? e : -e - 1
+  int k = 31 - __clz(u | 1u);
+  uint32_t delta = (uint32_t)((0x2C160B05020100ull >> (8 * k)) & 0xffu);
+  uint32_t thr = u < 2u ? 0x800000u : 0x800000u - delta;
+  int s = e + 119 + ((b & 0x7fffffu) >= thr ? 1 : 0);
+  return s < 0 ? 0u : (uint32_t)s;
+}
+
 // R1 E4M3 element code of an already scaled value (integer formulation).
 __device__ __forceinline__ uint32_t e4m3_code(float y) {
   uint32_t b = __float_as_uint(y);

@@ -153,7 +153,7 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_requant_p_rows(const floa
   a = fmaxf(a, __shfl_xor(a, 1));
   a = fmaxf(a, __shfl_xor(a, 2));
   a = fmaxf(a, __shfl_xor(a, 4));
-  uint32_t sc = scale_code_alu(a, 8);
+  uint32_t sc = scale_code_p(a);
   reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = r1_pack4(v.x, v.y, v.z, v.w, 127 - (int)sc);
   if (part == 0) scales[blk] = (uint8_t)sc;
 }
@@ -323,9 +323,19 @@ struct WaveState {
 
 // One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
 // mask: 0 = every key visible for every query of the wave; 1 = evaluate the mask.
+// Visible keys of one query row: [klo, khi] (khi < klo when none), folding the causal
+// limit, the sliding window, seq_k and row validity.
+__device__ __forceinline__ void key_limits(const FaArgs& a, int qpos, bool qvalid, int& klo, int& khi) {
+  khi = a.Sk - 1;
+  if (a.causal) khi = min(khi, qpos);
+  klo = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
+  if (!qvalid) khi = -1;
+}
+
+// mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
 template <int D, bool SOFTCAP>
 __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
-                                           const uint8_t* sVs, int key0, int qpos, bool qvalid, bool mask,
+                                           const uint8_t* sVs, int key0, int klo, int khi, bool mask,
                                            const FaArgs& a, int lane) {
   constexpr int KP = Lds<D>::KP;
   constexpr int KPB = Lds<D>::KPB;
@@ -344,27 +354,37 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   }
 
   // ---- scores in log2 units (softcap) or raw units, masked -> -inf
+  if (SOFTCAP) {
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        float u = s[t][i] * a.sc_u;
+        float e = __builtin_amdgcn_exp2f(-2.0f * LOG2E_F * fabsf(u));
+        float th = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+        s[t][i] = a.cap_log2 * (u < 0.0f ? -th : th);
+      }
+  }
+  if (mask) {
+    // The empty asm keeps this pass behind the (wave-uniform) branch: without it the
+    // selects are speculated into every block.
+    __asm__ volatile("");
+    const int dhi = khi - key0 - 4 * h, dlo = klo - key0 - 4 * h;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        // kpos - key0 - 4h is a compile-time constant per (t, i): two compares per element
+        const int c = 32 * t + 8 * (i >> 2) + (i & 3);
+        s[t][i] = (c <= dhi) & (c >= dlo) ? s[t][i] : -INFINITY;
+      }
+  }
   float tmax[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      float x = s[t][i];
-      if (SOFTCAP) {
-        float u = x * a.sc_u;
-        float e = __builtin_amdgcn_exp2f(-2.0f * LOG2E_F * fabsf(u));
-        float th = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
-        x = a.cap_log2 * (u < 0.0f ? -th : th);
-      }
-      if (mask) {
-        int kpos = key0 + 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
-        bool vis = qvalid && kpos < a.Sk && (!a.causal || kpos <= qpos) && (a.window <= 0 || kpos + a.window > qpos);
-        x = vis ? x : -INFINITY;
-      }
-      s[t][i] = x;
-      mx = fmaxf(mx, x);
-    }
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[t][i]);
     tmax[t] = mx;
   }
   // block (query, 32-key tile) maxima: combine the lane pair (l, l^32)
@@ -390,12 +410,12 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   // which leaves its code unchanged.
   const float mcn = -(mu * c);
   float lsum = 0.0f;
-  uint32_t pc[NT][4];
+  v8i pb[NT / 2];                    // P codes: B operand of each 64-key PV step
   int psc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     float amax = __builtin_amdgcn_exp2f((bmax[t] - mu) * c);
-    uint32_t sc = scale_code_alu(amax, 8);
+    uint32_t sc = scale_code_p(amax);
     int sh = 127 - (int)sc;
     psc[t] = (int)sc;
     float p[16];
@@ -405,7 +425,8 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
       lsum += p[i];
     }
 #pragma unroll
-    for (int g = 0; g < 4; g++) pc[t][g] = r1_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], sh);
+    for (int g = 0; g < 4; g++)
+      pb[t >> 1][4 * (t & 1) + g] = (int)r1_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], sh);
   }
   st.l = st.l * corr + lsum;
 
@@ -421,8 +442,6 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   const int l16 = lane & 15, g16 = lane >> 4;
 #pragma unroll
   for (int kstep = 0; kstep < BN / 64; kstep++) {
-    v8i pb = {(int)pc[2 * kstep][0], (int)pc[2 * kstep][1], (int)pc[2 * kstep][2], (int)pc[2 * kstep][3],
-              (int)pc[2 * kstep + 1][0], (int)pc[2 * kstep + 1][1], (int)pc[2 * kstep + 1][2], (int)pc[2 * kstep + 1][3]};
     int pscale = psc[2 * kstep + h];
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++) {
@@ -438,7 +457,7 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
         va[2 * q + 1] = rv[1];
       }
       int vscale = sVs[(2 * kstep + h) * D + dt * 32 + r];
-      st.o[dt] = mfma_mx(va, pb, st.o[dt], vscale, pscale);
+      st.o[dt] = mfma_mx(va, pb[kstep], st.o[dt], vscale, pscale);
     }
   }
 }
@@ -469,7 +488,9 @@ __device__ void prefill_impl(const FaArgs& a) {
   __shared__ __attribute__((aligned(16))) uint8_t sV[2][Lds<D>::TILE];
   __shared__ __attribute__((aligned(16))) uint8_t sVs[2][Lds<D>::SC];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave index through readfirstlane: everything derived from it stays in SGPRs and the
+  // per-block branches below are uniform
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
   // renumber them so that each XCD receives a contiguous range of work items, i.e.
@@ -494,6 +515,8 @@ __device__ void prefill_impl(const FaArgs& a) {
   const int64_t bh = (int64_t)b * a.Hq + head;
   v4i qb[D / 16];
   load_q<D>(qb, a.q + (bh * a.Sq + qi) * D, a.qs + (bh * a.Sq + qi) * (D / 32), qvalid, h);
+  int klo, khi;
+  key_limits(a, qpos, qvalid, klo, khi);
 
   // key-block range of the workgroup
   const int qmax_wg = min(q0 + a.qpw, a.Sq) - 1;
@@ -520,9 +543,10 @@ __device__ void prefill_impl(const FaArgs& a) {
     const int key0 = j * BN, key1 = key0 + BN - 1;
     bool skip = !wave_live || (a.causal && key0 > wq_hi) || (a.window > 0 && key1 + a.window <= wq_lo);
     if (!skip) {
-      bool need_mask = (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
-                       (qw0 + 31 >= a.Sq);
-      wave_block<D, SOFTCAP>(st, qb, sK[buf], sV[buf], sVs[buf], key0, qpos, qvalid, need_mask, a, lane);
+      const bool need_mask = __builtin_amdgcn_readfirstlane(
+          (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
+          (qw0 + 31 >= a.Sq));
+      wave_block<D, SOFTCAP>(st, qb, sK[buf], sV[buf], sVs[buf], key0, klo, khi, need_mask, a, lane);
     }
   };
   if constexpr (D <= 128) {
@@ -602,9 +626,9 @@ __device__ void decode_impl(const FaArgs& a) {
   __shared__ __attribute__((aligned(16))) uint8_t sK[NW][Lds<D>::TILEK];
   __shared__ __attribute__((aligned(16))) uint8_t sV[NW][Lds<D>::TILE];
   __shared__ __attribute__((aligned(16))) uint8_t sVs[NW][Lds<D>::SC];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
-  const int part = blockIdx.x * NW + (threadIdx.x >> 6);
+  const int part = blockIdx.x * NW + wave;
   const int bk = blockIdx.y;
   if (part >= a.n_qblk) return;                       // waves past the last chunk have no work
   const int b = bk / a.Hkv, kvh = bk % a.Hkv;
@@ -623,6 +647,9 @@ __device__ void decode_impl(const FaArgs& a) {
 
   const int kbeg = part * a.split_len;
   const int kend = min(kbeg + a.split_len, a.Sk);
+  int klo, khi;
+  key_limits(a, qpos, qvalid, klo, khi);
+  khi = min(khi, kend - 1);                          // the rest of the tile belongs to other chunks
 
   WaveState<D> st;
 #pragma unroll
@@ -668,8 +695,8 @@ __device__ void decode_impl(const FaArgs& a) {
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    const bool need_mask = true;           // columns >= group are padding and must be masked
-    wave_block<D, SOFTCAP>(st, qb, sK[wave], sV[wave], sVs[wave], key0, qpos, qvalid, need_mask, a, lane);
+    // columns >= group are padding and must be masked
+    wave_block<D, SOFTCAP>(st, qb, sK[wave], sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
     __builtin_amdgcn_wave_barrier();
   }
 
