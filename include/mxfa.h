@@ -107,13 +107,18 @@ mxfa_status mxfa_decode(const mxfa_attn_params *p,
                         const uint8_t *v_cache, const uint8_t *v_sc,
                         float *o, void *workspace, size_t workspace_bytes, void *stream);
 
-/* The attention kernels' P requantization routine on caller-supplied fp32 P
- * (finite, >= 0), 32-blocks along rows: codes [rows][cols], scales [rows][cols/32].
- * Replaces fused_softmax_requant's requant stage (kernels/flash_attention_mx_gqa/
- * flash_mx_impl.hpp:315-394) with rule R1 (lib/golden/mx_golden.cpp:146-190);
- * exposed so the routine can be checked bit-exactly in isolation. */
-mxfa_status mxfa_requant_p(const float *p, int64_t rows, int32_t cols,
-                           uint8_t *codes, uint8_t *scales, void *stream);
+/* The attention kernels' softmax-requant step on caller scores, exposed so that it can
+ * be checked bit-exactly in isolation.  Replaces fused_softmax_requant
+ * (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:315-394) with rule R1
+ * (lib/golden/mx_golden.cpp:146-190).  s [rows][cols] (cols % 32 == 0) are scores in the
+ * units of c (P = 2^((s - row_max) * c)), row_max [rows] >= every score of its row.  Per
+ * 32-block of a row: sc = R1 scale of amax = 2^((block max - row_max) * c) (exactly 1
+ * where the block holds the row max), codes = R1 E4M3 codes of P * 2^(127 - sc).
+ * Outputs p [rows][cols] (P as computed on the device), codes [rows][cols],
+ * scales [rows][cols/32], row_sum [rows] = sum of P. */
+mxfa_status mxfa_softmax_requant(const float *s, const float *row_max, float c, int64_t rows,
+                                 int32_t cols, float *p, uint8_t *codes, uint8_t *scales,
+                                 float *row_sum, void *stream);
 
 /* Synthetic inputs: x[i] ~ N(0,1) (counter-based hash + Box-Muller), each element
  * multiplied by outlier_mul with probability outlier_p.  Replaces make_inputs /

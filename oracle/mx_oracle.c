@@ -463,3 +463,7 @@ int64_t orc_check_log2_vs_libm(uint32_t lo, uint32_t hi) {
 void orc_e4m3_encode_range(uint32_t bits_lo, uint32_t count, uint8_t *out) {
   for (uint32_t i = 0; i < count; i++) out[i] = orc_e4m3_encode(u2f(bits_lo + i));
 }
+
+void orc_e4m3_encode_array(const float *x, int64_t n, uint8_t *out) {
+  for (int64_t i = 0; i < n; i++) out[i] = orc_e4m3_encode(x[i]);
+}

@@ -108,6 +108,7 @@ int orc_attention_dense(const orc_attn_params *p,
 /* Self-checks used by the tests. */
 int64_t orc_check_log2_vs_libm(uint32_t lo, uint32_t hi);
 void    orc_e4m3_encode_range(uint32_t bits_lo, uint32_t count, uint8_t *out);
+void    orc_e4m3_encode_array(const float *x, int64_t n, uint8_t *out);   /* orc_e4m3_encode per element */
 
 #ifdef __cplusplus
 }

@@ -64,6 +64,7 @@ def lib():
         L.orc_check_log2_vs_libm.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
         L.orc_check_log2_vs_libm.restype = ctypes.c_int64
         L.orc_e4m3_encode_range.argtypes = [ctypes.c_uint32, ctypes.c_uint32, P(ctypes.c_uint8)]
+        L.orc_e4m3_encode_array.argtypes = [f32p, ctypes.c_int64, u8p]
         _lib = L
     return _lib
 
@@ -116,9 +117,11 @@ def quantize_cols(x, fmt):
 
 
 def e4m3_encode(x):
-    x = np.asarray(x, dtype=np.float32).ravel()
-    f = lib().orc_e4m3_encode
-    return np.array([f(float(v)) for v in x], np.uint8)
+    """R1 E4M3 codes of already scaled float32 values (same shape as x)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().orc_e4m3_encode_array(_f32(x), x.size, _u8(out))
+    return out
 
 
 def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0, v_fmt=FMT_E4M3):

@@ -21,10 +21,6 @@ namespace mxfa {
 __constant__ uint32_t c_log2_thr[256] = MXFA_LOG2_THR_INIT;
 __constant__ uint32_t c_log2_sub_thr[23] = MXFA_LOG2_SUB_THR_INIT;
 
-// F4M3: the smallest float whose floorf(log2f()) is >= -6.  Scaled E4M3 inputs
-// below it flush to 0 under R1.
-constexpr uint32_t kE4M3FlushBits = (120u << 23) | 0x7ffffeu;
-
 // floorf(log2f(x)) for finite x > 0 (x == 0 returns a large negative number).
 __device__ __forceinline__ int floor_log2f(float x) {
   uint32_t b = __float_as_uint(x) & 0x7fffffffu;
@@ -37,21 +33,6 @@ __device__ __forceinline__ int floor_log2f(float x) {
   return (int)E - 127 + (m >= c_log2_thr[E] ? 1 : 0);
 }
 
-// floorf(log2f(x)) for finite x > 0 without a memory table: for a normal x with
-// exponent e the result is e + 1 when the mantissa reaches 2^23 - delta, where
-// delta depends only on the binade of u = (e >= 0 ? e : -e - 1) (log2f rounds to
-// the float grid around the integer e + 1); subnormals use the table.
-__device__ __forceinline__ int floor_log2f_alu(float x) {
-  uint32_t b = __float_as_uint(x) & 0x7fffffffu;
-  int e = (int)(b >> 23) - 127;
-  if (e == -127) return floor_log2f(x);
-  uint32_t u = e >= 0 ? (uint32_t)e : (uint32_t)(-e - 1);
-  int k = 31 - __clz(u | 1u);
-  uint32_t delta = (uint32_t)((0x2C160B05020100ull >> (8 * k)) & 0xffu);
-  uint32_t thr = u < 2u ? 0x800000u : 0x800000u - delta;
-  return e + ((b & 0x7fffffu) >= thr ? 1 : 0);
-}
-
 // E8M0 block scale code; amax = max |x| over the block (NaN already dropped by fmaxf).
 __device__ __forceinline__ uint32_t scale_code(float amax, int log2_pmax) {
   if (!(amax > 0.0f) || __builtin_isinf(amax)) return 0u;
@@ -59,17 +40,12 @@ __device__ __forceinline__ uint32_t scale_code(float amax, int log2_pmax) {
   return (uint32_t)(s2 < 0 ? 0 : (s2 > 254 ? 254 : s2));
 }
 
-// Same rule without the memory table (the attention kernels' P blocks).
-__device__ __forceinline__ uint32_t scale_code_alu(float amax, int log2_pmax) {
-  if (!(amax > 0.0f) || __builtin_isinf(amax)) return 0u;
-  int s2 = floor_log2f_alu(amax) - log2_pmax + 127;
-  return (uint32_t)(s2 < 0 ? 0 : (s2 > 254 ? 254 : s2));
-}
-
-// E4M3 block scale code of a finite amax >= 0 (the P blocks), without branches:
-// an amax below 2^-119 (zero and subnormals included) has floor(log2f) - 8 + 127 < 0,
-// i.e. code 0, so the subnormal table is never needed; finite amax stays below the
-// 254 clamp.
+// E4M3 block scale code of a finite amax >= 0 (the P blocks), without a table or
+// branches.  For a normal amax with exponent e, floorf(log2f(amax)) is e + 1 when the
+// mantissa reaches 2^23 - delta, where delta depends only on the binade of
+// u = (e >= 0 ? e : -e - 1) (log2f rounds to the float grid around e + 1).  An amax
+// below 2^-119 (zero and subnormals included) gives floor - 8 + 127 < 0, i.e. code 0,
+// and a finite amax stays below the 254 clamp.
 __device__ __forceinline__ uint32_t scale_code_p(float amax) {
   uint32_t b = __float_as_uint(amax);
   int e = (int)(b >> 23) - 127;
@@ -151,24 +127,43 @@ __device__ __forceinline__ uint32_t e3m2x4_to_e4m3x4(uint32_t w) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast R1 requant of non-negative, finite fp32 values (the attention P tiles).
-// y = p * 2^(127 - sc) is exact (power-of-two scaling of a value below 512);
-// R1 flushes y below F4M3 and saturates at 448; in between the hardware
-// conversion (RNE, OCP E4M3) gives the R1 code, including for y just below a
-// power of two where log2f rounds up.
+// R1 requant of the attention P tiles without rescaling P first.  With sh = 127 - sc,
+// R1 encodes y = P * 2^sh: zero below F4M3 (the smallest float whose floorf(log2f())
+// is >= -6), 448 from 448 up, RNE on the E4M3 grid in between.  The per-tile bounds
+// are moved to the P side (exact power-of-two scalings): flush below F4M3 * 2^-sh --
+// for sh >= 120 that bound is below 2^-126 and no nonzero P of an exponential (which
+// returns 0 below 2^-126) reaches it -- and cap at 448 * 2^-sh.  The conversion then
+// divides by its scale operand; it uses only that operand's exponent field (measured on
+// gfx950: 1.5 acts as 1, 3.0 as 2, and a float with exponent field 0 as 2^-127), so
+// (sc << 23) | 0x400000 is 2^(sc - 127) for every code, sc = 0 included.
 // ---------------------------------------------------------------------------
-typedef short v2s_t __attribute__((ext_vector_type(2)));
+constexpr uint32_t kE4M3FlushBits = (120u << 23) | 0x7ffffeu;   // F4M3
+constexpr uint32_t k448Bits = 0x43e00000u;
 
-__device__ __forceinline__ float r1_prep(float p, int sh) {
-  float y = __builtin_ldexpf(p, sh);
-  y = y < __uint_as_float(kE4M3FlushBits) ? 0.0f : y;
-  return __builtin_fminf(y, 448.0f);
+struct PTileBounds {
+  float flush, cap, scale;
+};
+
+__device__ __forceinline__ PTileBounds p_tile_bounds(uint32_t sc) {
+  const uint32_t sh = 127u - sc;
+  PTileBounds b;
+  b.flush = __uint_as_float(sc >= 8u ? kE4M3FlushBits - (sh << 23) : 0u);
+  b.cap = __uint_as_float(k448Bits - (sh << 23));
+  b.scale = __uint_as_float((sc << 23) | 0x400000u);
+  return b;
 }
 
-__device__ __forceinline__ uint32_t r1_pack4(float p0, float p1, float p2, float p3, int sh) {
+typedef short v2s_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float p_bound(float p, const PTileBounds& b) {
+  return __builtin_fminf(p < b.flush ? 0.0f : p, b.cap);
+}
+
+// Four P values (>= 0, finite) of one tile -> their R1 E4M3 codes (byte i = value i).
+__device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
   v2s_t pk = {0, 0};
-  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, r1_prep(p0, sh), r1_prep(p1, sh), 1.0f, false);
-  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, r1_prep(p2, sh), r1_prep(p3, sh), 1.0f, true);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, p_bound(p0, b), p_bound(p1, b), b.scale, false);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, p_bound(p2, b), p_bound(p3, b), b.scale, true);
   return (uint32_t)(uint16_t)pk[0] | ((uint32_t)(uint16_t)pk[1] << 16);
 }
 

@@ -37,7 +37,7 @@ mxfa_status fail(mxfa_status st, const std::string& msg) {
 
 const char* const kKernelNames[] = {
     "mxfa_quant_rows_e4m3",    "mxfa_quant_rows_e3m2",    "mxfa_quant_cols_e4m3", "mxfa_quant_cols_e3m2",
-    "mxfa_requant_p_rows",     "mxfa_fill_normal_f32",    "mxfa_prefill_d64",     "mxfa_prefill_d128",
+    "mxfa_softmax_requant_rows",     "mxfa_fill_normal_f32",    "mxfa_prefill_d64",     "mxfa_prefill_d128",
     "mxfa_prefill_d256",       "mxfa_prefill_d64_softcap", "mxfa_prefill_d128_softcap", "mxfa_prefill_d256_softcap",
     "mxfa_decode_d64",         "mxfa_decode_d128",        "mxfa_decode_d256",     "mxfa_decode_d64_softcap",
     "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine",
@@ -246,18 +246,20 @@ mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32
   return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : "mxfa_quant_cols_e3m2", grid, dim3(256), args, stream);
 }
 
-mxfa_status mxfa_requant_p(const float* p, int64_t rows, int32_t cols, uint8_t* codes, uint8_t* scales, void* stream) {
+mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, int64_t rows, int32_t cols,
+                                 float* p, uint8_t* codes, uint8_t* scales, float* row_sum, void* stream) {
   if (rows < 0 || cols <= 0 || cols % 32) return fail(MXFA_ERR_INVALID_ARG, "cols must be a positive multiple of 32");
+  if (!(c > 0.0f) || !std::isfinite(c)) return fail(MXFA_ERR_INVALID_ARG, "c must be finite and > 0");
   if (rows == 0) return MXFA_OK;
-  if (!p || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
-  if (!aligned16(p) || (reinterpret_cast<uintptr_t>(codes) & 3u))
-    return fail(MXFA_ERR_INVALID_ARG, "p must be 16-byte and codes 4-byte aligned");
+  if (!s || !row_max || !p || !codes || !scales || !row_sum) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  if (!aligned16(s) || (reinterpret_cast<uintptr_t>(codes) & 3u))
+    return fail(MXFA_ERR_INVALID_ARG, "s must be 16-byte and codes 4-byte aligned");
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
-  int64_t nblocks = rows * (int64_t)cols / 32;
-  dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
-  void* args[] = {(void*)&p, &nblocks, &codes, &scales};
-  return launch(dm, "mxfa_requant_p_rows", grid, dim3(256), args, stream);
+  dim3 grid((unsigned)((rows + 255) / 256));
+  int cols_i = cols;
+  void* args[] = {(void*)&s, (void*)&row_max, &c, &rows, &cols_i, &p, &codes, &scales, &row_sum};
+  return launch(dm, "mxfa_softmax_requant_rows", grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p, float outlier_mul, void* stream) {

@@ -140,24 +140,6 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e3m2(const flo
   quant_cols_impl<1>(x, mats, rows, cols, codes, scales);
 }
 
-// The attention kernels' P requant routine on caller-supplied fp32 P (>= 0,
-// finite), 32-blocks along rows: used by the tests to pin it bit-exactly.
-extern "C" __global__ void __launch_bounds__(256) mxfa_requant_p_rows(const float* p, int64_t nblocks,
-                                                                      uint8_t* codes, uint8_t* scales) {
-  int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t blk = gt >> 3;
-  int part = (int)(gt & 7);
-  if (blk >= nblocks) return;
-  float4 v = reinterpret_cast<const float4*>(p)[blk * 8 + part];
-  float a = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-  a = fmaxf(a, __shfl_xor(a, 1));
-  a = fmaxf(a, __shfl_xor(a, 2));
-  a = fmaxf(a, __shfl_xor(a, 4));
-  uint32_t sc = scale_code_p(a);
-  reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = r1_pack4(v.x, v.y, v.z, v.w, 127 - (int)sc);
-  if (part == 0) scales[blk] = (uint8_t)sc;
-}
-
 // ============================================================================
 // Synthetic inputs: x[i] ~ N(0,1) from a counter-based hash (splitmix64) and
 // Box-Muller; each element independently multiplied by `mul` with probability p.
@@ -332,6 +314,72 @@ __device__ __forceinline__ void key_limits(const FaArgs& a, int qpos, bool qvali
   if (!qvalid) khi = -1;
 }
 
+// ---- softmax-requant of one P tile (the reference's fused_softmax_requant,
+// kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:315-394, with rule R1).
+// Scale: the tile amax is exp2((tile max - m) * c) -- exactly 1 in the tile holding
+// the row max, like the reference's exp(S - m) -- and sc its R1 code.  P =
+// exp2(fma(s, c, -m*c)); fma and exp2 are monotone, so no P of the tile exceeds the amax
+// by more than one rounding residue, which leaves its code unchanged.
+__device__ __forceinline__ uint32_t p_tile_scale(float bmax, float mu, float c) {
+  return scale_code_p(__builtin_amdgcn_exp2f((bmax - mu) * c));
+}
+
+// 16 P values of one lane: writes P and the codes (w[g] byte j = value 4g + j), adds
+// the P values to lsum in order.
+__device__ __forceinline__ void p_tile16(const v16f& s, float c, float mcn, uint32_t sc, float (&p)[16],
+                                         uint32_t (&w)[4], float& lsum) {
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c, mcn));
+    lsum += p[i];
+  }
+  const PTileBounds bnd = p_tile_bounds(sc);
+#pragma unroll
+  for (int g = 0; g < 4; g++) w[g] = p_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], bnd);
+}
+
+// Test entry: the routine above on caller scores, one thread per row, 32-blocks along
+// the row.  Outputs P, codes, scales, and the row sums of P.
+extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
+    const float* s, const float* row_max, float c, int64_t rows, int cols, float* p, uint8_t* codes,
+    uint8_t* scales, float* row_sum) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float mu = row_max[r], mcn = -(mu * c);
+  float lsum = 0.0f;
+  for (int j = 0; j < cols / 32; j++) {
+    const int64_t off = r * cols + 32 * j;
+    v16f a, b;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float4 x = reinterpret_cast<const float4*>(s + off)[i];
+      float4 y = reinterpret_cast<const float4*>(s + off)[4 + i];
+      a[4 * i] = x.x; a[4 * i + 1] = x.y; a[4 * i + 2] = x.z; a[4 * i + 3] = x.w;
+      b[4 * i] = y.x; b[4 * i + 1] = y.y; b[4 * i + 2] = y.z; b[4 * i + 3] = y.w;
+    }
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; i++) bmax = fmaxf(bmax, fmaxf(a[i], b[i]));
+    const uint32_t sc = p_tile_scale(bmax, mu, c);
+    float pa[16], pb[16];
+    uint32_t wa[4], wb[4];
+    p_tile16(a, c, mcn, sc, pa, wa, lsum);
+    p_tile16(b, c, mcn, sc, pb, wb, lsum);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      p[off + i] = pa[i];
+      p[off + 16 + i] = pb[i];
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      reinterpret_cast<uint32_t*>(codes + off)[g] = wa[g];
+      reinterpret_cast<uint32_t*>(codes + off)[4 + g] = wb[g];
+    }
+    scales[r * (cols / 32) + j] = (uint8_t)sc;
+  }
+  row_sum[r] = lsum;
+}
+
 // mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
 template <int D, bool SOFTCAP>
 __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
@@ -404,29 +452,20 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   float corr = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((st.m - mu) * c);
   st.m = m_new;
 
-  // ---- P = exp2(fma(x, c, -m*c)); the per-tile amax is exp2((tile max - m) * c), exactly
-  // 1 in the tile holding the row max.  fma and exp2 are monotone, so the amax bounds every
-  // P of the tile; a P at the row max may exceed it by one rounding residue (< 2^-16),
-  // which leaves its code unchanged.
+  // ---- P tiles: scale from the exact tile amax, R1 codes
   const float mcn = -(mu * c);
   float lsum = 0.0f;
   v8i pb[NT / 2];                    // P codes: B operand of each 64-key PV step
   int psc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
-    float amax = __builtin_amdgcn_exp2f((bmax[t] - mu) * c);
-    uint32_t sc = scale_code_p(amax);
-    int sh = 127 - (int)sc;
+    const uint32_t sc = p_tile_scale(bmax[t], mu, c);
     psc[t] = (int)sc;
     float p[16];
+    uint32_t w[4];
+    p_tile16(s[t], c, mcn, sc, p, w, lsum);
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], c, mcn));
-      lsum += p[i];
-    }
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-      pb[t >> 1][4 * (t & 1) + g] = (int)r1_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], sh);
+    for (int g = 0; g < 4; g++) pb[t >> 1][4 * (t & 1) + g] = (int)w[g];
   }
   st.l = st.l * corr + lsum;
 

@@ -11,7 +11,7 @@ vocabulary on top of the C ABI:
     quantize_cols     -> mx_quantize_cols(V.t()) (32-blocks along the key axis)
     prefill           -> mx_attention_flash[_causal_gqa | _gemma]
     decode            -> the same recurrence over an MXFP8 KV cache (split-KV)
-    requant_p         -> the P requant step of fused_softmax_requant
+    softmax_requant   -> fused_softmax_requant (the P tile step, for bit-exact checks)
 
 torch is used only to hold device memory and name the stream; every call goes through
 ctypes into libmxfa.so, which launches gfx950 kernels.  There is no fallback: if the
@@ -56,7 +56,7 @@ def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=N
 
 
 EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
-           "mxfa_requant_p", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
+           "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
            "mxfa_last_error", "mxfa_version")
 
 _lib = None
@@ -76,14 +76,15 @@ def lib():
         L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
         L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
         L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
-        L.mxfa_requant_p.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, u8p, u8p, vp]
+        L.mxfa_softmax_requant.argtypes = [f32p, f32p, ctypes.c_float, ctypes.c_int64, ctypes.c_int32, f32p,
+                                           u8p, u8p, f32p, vp]
         L.mxfa_fill_normal.argtypes = [f32p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp]
         L.mxfa_status_string.argtypes = [ctypes.c_int]
         L.mxfa_status_string.restype = ctypes.c_char_p
         L.mxfa_last_error.restype = ctypes.c_char_p
         L.mxfa_version.restype = ctypes.c_int32
         for name in ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
-                     "mxfa_requant_p", "mxfa_fill_normal", "mxfa_init"):
+                     "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -134,15 +135,23 @@ def quantize_cols(x, fmt=FMT_E4M3, stream=None):
     return codes, scales
 
 
-def requant_p(p, stream=None):
+def softmax_requant(s, row_max, c, stream=None):
+    """The kernels' softmax-requant step on scores s [..., cols] (cols % 32 == 0) with
+    per-row maxima row_max [...]: returns (p, codes, scales, row_sum)
+    (mxfa_softmax_requant)."""
     import torch
-    assert p.is_cuda and p.dtype == torch.float32 and p.is_contiguous()
-    cols = p.shape[-1]
-    rows = p.numel() // cols
-    codes = torch.empty(p.shape, dtype=torch.uint8, device=p.device)
-    scales = torch.empty(tuple(p.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=p.device)
-    _check(lib().mxfa_requant_p(_ptr(p), rows, cols, _ptr(codes), _ptr(scales), _stream(stream)))
-    return codes, scales
+    assert s.is_cuda and s.dtype == torch.float32 and s.is_contiguous()
+    assert row_max.is_cuda and row_max.dtype == torch.float32 and row_max.is_contiguous()
+    cols = s.shape[-1]
+    rows = s.numel() // cols
+    assert row_max.numel() == rows
+    p = torch.empty_like(s)
+    codes = torch.empty(s.shape, dtype=torch.uint8, device=s.device)
+    scales = torch.empty(tuple(s.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=s.device)
+    row_sum = torch.empty(tuple(s.shape[:-1]), dtype=torch.float32, device=s.device)
+    _check(lib().mxfa_softmax_requant(_ptr(s), _ptr(row_max), float(c), rows, cols, _ptr(p), _ptr(codes),
+                                      _ptr(scales), _ptr(row_sum), _stream(stream)))
+    return p, codes, scales, row_sum
 
 
 def fill_normal(x, seed, outlier_p=0.0, outlier_mul=20.0, stream=None):

@@ -31,7 +31,7 @@ def test_code_object_present_and_for_gfx950():
     data = open(path, "rb").read()
     assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     assert b"gfx950" in data
-    for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_requant_p_rows"):
+    for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows"):
         assert k.encode() in data
 
 
@@ -97,4 +97,6 @@ def test_quantize_argument_validation():
     assert L.mxfa_quantize_rows(None, 0, 64, 0, None, None, None) == 0     # empty input: no-op
     assert L.mxfa_quantize_cols(None, 1, 48, 64, 0, None, None, None) == 1
     assert L.mxfa_quantize_cols(None, 0, 64, 64, 0, None, None, None) == 0
-    assert L.mxfa_requant_p(None, 4, 33, None, None, None) == 1
+    assert L.mxfa_softmax_requant(None, None, 1.0, 4, 33, None, None, None, None, None) == 1
+    assert L.mxfa_softmax_requant(None, None, 0.0, 4, 32, None, None, None, None, None) == 1
+    assert L.mxfa_softmax_requant(None, None, 1.0, 0, 32, None, None, None, None, None) == 0

@@ -1,4 +1,4 @@
-"""GPU parity of the MX quantizers and of the attention kernels' P requant routine:
+"""GPU parity of the MX quantizers and of the attention kernels' softmax-requant step:
 bit-exact against the oracle (rule R1 of lib/golden, pinned in test_oracle_rules)."""
 import numpy as np
 import pytest
@@ -80,34 +80,73 @@ def test_e3m2_quantizer_covers_all_bf16_magnitudes_below_32():
     np.testing.assert_array_equal(np_(codes), want[vb])
 
 
-def p_like(rng, rows):
-    """fp32 P tiles as the attention kernels produce them: exp2 of non-positive arguments,
-    plus zero blocks, subnormals, and values on the flush/saturation/rounding edges."""
-    x = np.exp2(-rng.exponential(6.0, (rows, 64))).astype(np.float32)
-    x[rng.random(x.shape) < 0.05] = 0.0
-    x[::17] = 0.0
-    x[5::23, :32] *= np.float32(2.0 ** -130)                   # subnormal blocks
-    edge = []
-    for e in range(-40, 1):
-        m = np.float32(2.0 ** e)
-        r = m * np.float32(2.0 ** -14) * (1 + np.arange(64, dtype=np.float32) / 64)
-        r[0] = m * np.float32(1.75)                              # saturation region after scaling
-        r[1] = m * np.float32(2.0 ** -6) * np.float32(0.9999999)
-        r[2] = m * np.float32(1.0 + 1.0 / 16)                    # RNE tie
-        r[32] = np.nextafter(m, np.float32(0))                   # block max just below a power of two
-        edge.append(r)
-    return np.concatenate([x, np.stack(edge)]).astype(np.float32)
+LOG2E = 1.4426950408889634
 
 
-def test_requant_p_bit_exact():
-    rng = np.random.default_rng(300)
-    p = p_like(rng, 8192)
-    pd = torch.from_numpy(p).to(DEV)
-    codes, scales = mxfa.requant_p(pd)
-    oc, osc = O.quantize_rows(p, O.FMT_E4M3)
-    np.testing.assert_array_equal(np_(scales), osc)
-    bad = np.argwhere(np_(codes) != oc)
-    assert len(bad) == 0, [(float(p[i, j]), int(np_(codes)[i, j]), int(oc[i, j])) for i, j in bad[:8]]
+def softmax_inputs(rng, rows, cols, c):
+    """Scores and row maxima as the attention kernels see them: N(0, sigma) rows with x20
+    outliers, -inf (masked) entries and whole masked blocks, row maxima above the row's
+    own max (a running max from earlier blocks), and blocks pushed 100-140 log2 units
+    below the row max (tiny and zero amax, scale codes near 0, k up to 7)."""
+    # spreads in exp2-argument units (x c), the same for every c
+    sig = (rng.choice([1.0, 5.0, 30.0], size=(rows, 1)) * (0.08838834764831845 * LOG2E / c)).astype(np.float32)
+    s = (rng.standard_normal((rows, cols)) * sig).astype(np.float32)
+    out = rng.random((rows, cols)) < 0.01
+    s[out] *= np.float32(20.0)
+    s[rng.random((rows, cols)) < 0.05] = -np.inf
+    nb = cols // 32
+    sb = s.reshape(rows, nb, 32)
+    sb[rng.random((rows, nb)) < 0.03] = -np.inf
+    far = rng.random((rows, nb)) < 0.1
+    shift = (rng.uniform(100.0, 140.0, size=(rows, nb)) / c).astype(np.float32)
+    sb[far] -= shift[far][:, None]
+    rmax = np.max(np.where(np.isfinite(s), s, -np.float32(1e30)), axis=1).astype(np.float32)
+    rmax[rmax < -1e29] = 0.0                               # fully masked row
+    bump = rng.random(rows) < 0.3
+    rmax[bump] += (rng.exponential(4.0, size=bump.sum()) / c).astype(np.float32)
+    return np.ascontiguousarray(s), rmax
+
+
+@pytest.mark.parametrize("c", [0.08838834764831845 * LOG2E, 0.125 * LOG2E, 1.0])
+def test_softmax_requant_bit_exact(c):
+    """The kernels' P tile step: codes are exactly R1's E4M3 codes of P * 2^(127 - sc) for
+    the P the device computed, sc is R1's scale of the tile amax (1 exactly in the row-max
+    tile), and P and the row sums are accurate."""
+    rng = np.random.default_rng(301)
+    rows, cols = 8192, 128
+    s, rmax = softmax_inputs(rng, rows, cols, c)
+    p, codes, scales, rsum = mxfa.softmax_requant(torch.from_numpy(s).to(DEV), torch.from_numpy(rmax).to(DEV), c)
+    p, codes, scales, rsum = (np_(t) for t in (p, codes, scales, rsum))
+    nb = cols // 32
+    assert np.all((p == 0) | (p >= np.float32(2.0 ** -126)))      # exp2 returns 0 below 2^-126
+    # element rule: R1 E4M3 of y = P * 2^(127 - sc) (exact power-of-two scaling)
+    sh = 127 - np.repeat(scales.astype(np.int32), 32, axis=1)
+    y = np.ldexp(p, sh).astype(np.float32)
+    want = O.e4m3_encode(y)
+    bad = np.argwhere(codes != want)
+    assert len(bad) == 0, [(float(y[i, j]), int(codes[i, j]), int(want[i, j])) for i, j in bad[:8]]
+    assert (sh >= 120).any() and (want == 0).any() and (want == 0x7e).any()   # flush, saturation, tiny tiles
+    # scale rule on the tile amax 2^((max s - m) c); the host exp2 may differ from the device
+    # one by an ulp, which can only matter within an ulp of a floor(log2f) step
+    bmax = s.reshape(rows, nb, 32).max(axis=2).astype(np.float64)
+    arg = (bmax - rmax[:, None].astype(np.float64)) * c
+    amax = np.exp2(arg).astype(np.float32)
+    ref_sc = np.array([[L_scale(a) for a in row] for row in amax], np.uint8)
+    lg = np.log2(np.maximum(amax, np.float32(1e-45)))
+    near = np.abs(lg - np.round(lg)) < 1e-6
+    mism = (scales != ref_sc) & ~near
+    assert not mism.any(), np.argwhere(mism)[:8]
+    assert np.all(scales[arg == 0.0] == 119)                 # the row-max tile: amax exactly 1
+    # P itself and the row sums
+    Pref = np.exp2((s.astype(np.float64) - rmax[:, None]) * c)
+    big = Pref > 2.0 ** -100
+    rel = np.abs(p[big] - Pref[big]) / Pref[big]
+    assert rel.max() < 1e-4, rel.max()
+    np.testing.assert_allclose(rsum, p.astype(np.float64).sum(axis=1), rtol=1e-5, atol=1e-30)
+
+
+def L_scale(a):
+    return O.lib().orc_scale_code(float(a), O.FMT_E4M3)
 
 
 def test_fill_normal_statistics():
