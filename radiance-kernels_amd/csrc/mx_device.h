@@ -161,7 +161,8 @@ __device__ __forceinline__ float p_bound(float p, const PTileBounds& b) {
 
 // Four P values (>= 0, finite) of one tile -> their R1 E4M3 codes (byte i = value i).
 __device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
-  v2s_t pk = {0, 0};
+  v2s_t pk;
+  pk = __builtin_nondeterministic_value(pk);        // both halves are written below
   pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, p_bound(p0, b), p_bound(p1, b), b.scale, false);
   pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, p_bound(p2, b), p_bound(p3, b), b.scale, true);
   return (uint32_t)(uint16_t)pk[0] | ((uint32_t)(uint16_t)pk[1] << 16);

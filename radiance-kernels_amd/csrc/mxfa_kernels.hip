@@ -237,34 +237,34 @@ template <int D> struct Lds {
   static constexpr int SC = BN * D / 32;
 };
 
+// Buffer resource over [base + off, base + off + bytes): loads beyond it return 0, so
+// key rows >= Sk need no branch.  Word 3 = raw 32-bit data format (gfx9 buffer layout).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const uint8_t* base, int64_t off, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), 0, (int)(bytes > 0 ? bytes : 0), 0x00020000);
+}
+
 // Global -> registers for key block starting at key0 (rows >= Sk read as 0).
 template <int D>
 __device__ __forceinline__ void load_block(BlockRegs<D>& r, const uint8_t* __restrict__ kb, const uint8_t* __restrict__ ksb,
                                            const uint8_t* __restrict__ vb, const uint8_t* __restrict__ vsb,
                                            int key0, int Sk, int tid) {
   constexpr int CPR = BlockRegs<D>::CPR;
+  const int nk = Sk - key0;
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kb, (int64_t)key0 * D, (int64_t)nk * D);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vb, (int64_t)key0 * D, (int64_t)nk * D);
+  const __amdgpu_buffer_rsrc_t rks = buf_rsrc(ksb, (int64_t)key0 * (D / 32), (int64_t)nk * (D / 32));
 #pragma unroll
   for (int i = 0; i < BlockRegs<D>::PER; i++) {
-    int c = tid + i * NWAVE * 64;
-    int row = c / CPR, col = (c % CPR) * 16;
-    int key = key0 + row;
-    v4i zk = {0, 0, 0, 0}, zv = {0, 0, 0, 0};
-    uint32_t ksc = 0;
-    if (key < Sk) {
-      zk = *reinterpret_cast<const v4i*>(kb + (int64_t)key * D + col);
-      zv = *reinterpret_cast<const v4i*>(vb + (int64_t)key * D + col);
-      ksc = ksb[(int64_t)key * (D / 32) + col / 32];
-    }
-    r.k[i] = zk;
-    r.kscale[i] = ksc;
-    r.v[i] = zv;
+    const int c = tid + i * NWAVE * 64;
+    const int row = c / CPR, col = (c % CPR) * 16;
+    r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, row * D + col, 0, 0);
+    r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, row * D + col, 0, 0);
+    r.kscale[i] = __builtin_amdgcn_raw_buffer_load_b8(rks, row * (D / 32) + col / 32, 0, 0);
   }
   constexpr int SCH = BlockRegs<D>::SCH;
-  r.vsc = (v4i){0, 0, 0, 0};
-  if (tid < SCH) {
-    int byte = tid * 16;                        // V scales: [key/32][D]
-    int kb32 = key0 / 32 + byte / D;
-    if (kb32 < Sk / 32) r.vsc = *reinterpret_cast<const v4i*>(vsb + (int64_t)(key0 / 32) * D + byte);
+  if (tid < SCH) {                                     // V scales: [key/32][D]
+    const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(vsb, (int64_t)(key0 / 32) * D, (int64_t)(Sk / 32 - key0 / 32) * D);
+    r.vsc = __builtin_amdgcn_raw_buffer_load_b128(rvs, tid * 16, 0, 0);
   }
 }
 
@@ -424,7 +424,7 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
       for (int i = 0; i < 16; i++) {
         // kpos - key0 - 4h is a compile-time constant per (t, i): two compares per element
         const int c = 32 * t + 8 * (i >> 2) + (i & 3);
-        s[t][i] = (c <= dhi) & (c >= dlo) ? s[t][i] : -INFINITY;
+        s[t][i] = ((c <= dhi) & (c >= dlo)) ? s[t][i] : -INFINITY;
       }
   }
   float tmax[NT];
