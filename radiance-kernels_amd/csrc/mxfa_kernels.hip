@@ -303,8 +303,6 @@ struct WaveState {
   float l;       // per-lane partial row sum (the partner lane holds the rest)
 };
 
-// One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
-// mask: 0 = every key visible for every query of the wave; 1 = evaluate the mask.
 // Visible keys of one query row: [klo, khi] (khi < klo when none), folding the causal
 // limit, the sliding window, seq_k and row validity.
 __device__ __forceinline__ void key_limits(const FaArgs& a, int qpos, bool qvalid, int& klo, int& khi) {
@@ -381,25 +379,31 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
 }
 
 // mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
-template <int D, bool SOFTCAP>
-__device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
-                                           const uint8_t* sVs, int key0, int klo, int khi, bool mask,
-                                           const FaArgs& a, int lane) {
-  constexpr int KP = Lds<D>::KP;
+// S^T = K Q^T (bf16 MFMA) for one 64-key block from the LDS K tile: tile t covers keys
+// 32t .. 32t+31.
+template <int D>
+__device__ __forceinline__ void qk_tiles(v16f (&s)[BN / 32], const v4i* qb, const uint8_t* sKb, int lane) {
   constexpr int KPB = Lds<D>::KPB;
-  constexpr int NT = BN / 32;
   const int r = lane & 31, h = lane >> 5;
-
-  // ---- S^T = K Q^T (bf16 MFMA): tile t covers keys key0 + 32t .. +31
-  v16f s[NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) {
+  for (int t = 0; t < BN / 32; t++) {
     s[t] = (v16f){};
     const uint8_t* krow = sKb + (t * 32 + r) * KPB + 16 * h;
 #pragma unroll
     for (int kk = 0; kk < D / 16; kk++)
       s[t] = mfma_bf16(*reinterpret_cast<const v4i*>(krow + 32 * kk), qb[kk], s[t]);
   }
+}
+
+// Softmax, P requant and O^T += V^T P^T for one key block whose scores are in s.
+// mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
+template <int D, bool SOFTCAP>
+__device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32], const uint8_t* sV,
+                                           const uint8_t* sVs, int key0, int klo, int khi, bool mask,
+                                           const FaArgs& a, int lane) {
+  constexpr int KP = Lds<D>::KP;
+  constexpr int NT = BN / 32;
+  const int r = lane & 31, h = lane >> 5;
 
   // ---- scores in log2 units (softcap) or raw units, masked -> -inf
   if (SOFTCAP) {
@@ -501,6 +505,16 @@ __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, cons
   }
 }
 
+// One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
+template <int D, bool SOFTCAP>
+__device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
+                                           const uint8_t* sVs, int key0, int klo, int khi, bool mask,
+                                           const FaArgs& a, int lane) {
+  v16f s[BN / 32];
+  qk_tiles<D>(s, qb, sKb, lane);
+  softmax_pv<D, SOFTCAP>(st, s, sV, sVs, key0, klo, khi, mask, a, lane);
+}
+
 // Q operand (B of S^T = K Q^T, bf16) for query row `qrow` (zeros if invalid): MFMA kk
 // takes d = 16*kk + 8*h .. +7, dequantized with the row's E8M0 scale of that 32-block.
 template <int D>
@@ -511,6 +525,24 @@ __device__ __forceinline__ void load_q(v4i* qb, const uint8_t* qrow, const uint8
     if (valid) {
       v2i w = *reinterpret_cast<const v2i*>(qrow + 16 * kk + 8 * h);
       o = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1], e8m0_as_float(qsrow[kk / 2]));
+    }
+    qb[kk] = o;
+  }
+}
+
+// Split-d operand mapping of the decode kernels: lane half h owns d in [h*D/2, (h+1)*D/2)
+// and MFMA kk takes d = h*D/2 + 8*kk .. +7 (any d-to-k assignment gives the same dot
+// product when Q and K use it alike).  A lane's K operand is then one contiguous
+// half-row of the key, read straight from global memory.
+template <int D>
+__device__ __forceinline__ void load_q_split(v4i* qb, const uint8_t* qrow, const uint8_t* qsrow, bool valid, int h) {
+#pragma unroll
+  for (int kk = 0; kk < D / 16; kk++) {
+    const int d0 = h * (D / 2) + 8 * kk;
+    v4i o = {0, 0, 0, 0};
+    if (valid) {
+      v2i w = *reinterpret_cast<const v2i*>(qrow + d0);
+      o = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1], e8m0_as_float(qsrow[d0 / 32]));
     }
     qb[kk] = o;
   }
@@ -656,6 +688,128 @@ MXFA_PREFILL(256, true, mxfa_prefill_d256_softcap)
 // (m, l, O); mxfa_decode_combine merges the partials in part order.  The
 // group's query heads are the wave's query columns (column c = head kvh*group + c).
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Decode, D <= 128.  One wave per chunk of split_len keys of one (b, KV head); its 32
+// score columns are the group's query heads (columns >= group are padding, masked).
+// K goes straight from global memory to registers in the split-d mapping and is
+// dequantized to bf16 right before each score MFMA; only V (transposed by the
+// ds_read_b64_tr_b8 reads of the PV step) passes through the wave's LDS slot.  Small
+// per-wave LDS and register footprints give two workgroups per CU, whose waves hide
+// each other's load latency.
+// ---------------------------------------------------------------------------
+template <int D, bool SOFTCAP>
+__device__ void decode_split_impl(const FaArgs& a) {
+  constexpr int NW = 4;
+  constexpr int NT = BN / 32;
+  constexpr int CPR = D / 16;                         // 16-byte chunks per V row
+  constexpr int PERW = BN * CPR / 64;                 // V chunks per lane
+  constexpr int SCW = BN * D / 32 / 4;                // V scale dwords per block
+  constexpr int KC = D / 32;                          // 16-byte K chunks per lane per tile
+  constexpr int KP = Lds<D>::KP;
+  __shared__ __attribute__((aligned(16))) uint8_t sV[NW][Lds<D>::TILE];
+  __shared__ __attribute__((aligned(16))) uint8_t sVs[NW][Lds<D>::SC];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int part = blockIdx.x * NW + wave;
+  const int bk = blockIdx.y;
+  if (part >= a.n_qblk) return;                       // waves past the last chunk have no work
+  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
+  const bool qvalid = r < a.group;
+  const int head = kvh * a.group + (qvalid ? r : 0);
+  const int64_t bh = (int64_t)b * a.Hq + head;
+  const int qpos = a.q_pos0;                          // the single query's position
+
+  v4i qb[D / 16];
+  load_q_split<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
+
+  // buffer resources end at Sk: rows past it read 0
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.k, (int64_t)bk * a.Sk * D, (int64_t)a.Sk * D);
+  const __amdgpu_buffer_rsrc_t rks = buf_rsrc(a.ks, (int64_t)bk * a.Sk * (D / 32), (int64_t)a.Sk * (D / 32));
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.v, (int64_t)bk * a.Sk * D, (int64_t)a.Sk * D);
+  const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(a.vs, (int64_t)bk * (a.Sk / 32) * D, (int64_t)(a.Sk / 32) * D);
+
+  const int kbeg = part * a.split_len;
+  const int kend = min(kbeg + a.split_len, a.Sk);
+  int klo, khi;
+  key_limits(a, qpos, qvalid, klo, khi);
+  khi = min(khi, kend - 1);                          // the rest of the tile belongs to other chunks
+
+  WaveState<D> st;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; dt++) st.o[dt] = (v16f){};
+  st.m = -INFINITY;
+  st.l = 0.0f;
+
+  for (int key0 = kbeg; key0 < kend; key0 += BN) {
+    // this lane's K half-rows (keys key0 + 32t + r) and their E8M0 scales
+    v4i kr[NT][KC];
+    uint32_t ksr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int row = key0 + 32 * t + r;
+#pragma unroll
+      for (int c = 0; c < KC; c++)
+        kr[t][c] = __builtin_amdgcn_raw_buffer_load_b128(rk, row * D + h * (D / 2) + 16 * c, 0, 0);
+      if constexpr (D == 128)
+        ksr[t] = __builtin_amdgcn_raw_buffer_load_b16(rks, row * 4 + 2 * h, 0, 0);
+      else
+        ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, row * 2 + h, 0, 0);
+    }
+    // V codes and scales -> the wave's LDS slot (E3M2 widened to E4M3)
+    v4i vr[PERW];
+#pragma unroll
+    for (int i = 0; i < PERW; i++) {
+      const int c = lane + 64 * i;
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, (key0 + c / CPR) * D + (c % CPR) * 16, 0, 0);
+    }
+    const uint32_t vsr = lane < SCW ? __builtin_amdgcn_raw_buffer_load_b32(rvs, (key0 / 32) * D + 4 * lane, 0, 0) : 0u;
+#pragma unroll
+    for (int i = 0; i < PERW; i++) {
+      const int c = lane + 64 * i;
+      v4i zv = vr[i];
+      if (a.v_e3m2) {
+#pragma unroll
+        for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
+      }
+      *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = zv;
+    }
+    if (lane < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * lane]) = vsr;
+    // scores from registers: K dequantized to bf16 just before each MFMA
+    v16f sc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      sc[t] = (v16f){};
+#pragma unroll
+      for (int kk = 0; kk < D / 16; kk++) {
+        const v4i& w = kr[t][kk / 2];
+        const float scale = e8m0_as_float((ksr[t] >> (8 * (kk / 4))) & 0xffu);
+        const v4i ka = fp8x8_to_bf16x8((uint32_t)w[2 * (kk & 1)], (uint32_t)w[2 * (kk & 1) + 1], scale);
+        sc[t] = mfma_bf16(ka, qb[kk], sc[t]);
+      }
+    }
+    // LDS operations of one wave complete in order: the V tile written above is in place
+    // for the transposed reads, and the next block's writes follow this block's reads
+    softmax_pv<D, SOFTCAP>(st, sc, sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
+  }
+
+  // partial outputs (unnormalized O, m in x units, full l)
+  float l = pair_sum(st.l);
+  const int nparts = a.n_qblk;
+  if (qvalid) {
+    float* po = a.part_o + (bh * nparts + part) * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *reinterpret_cast<float4*>(po + dt * 32 + 8 * g + 4 * h) =
+            make_float4(st.o[dt][4 * g], st.o[dt][4 * g + 1], st.o[dt][4 * g + 2], st.o[dt][4 * g + 3]);
+    if (h == 0) {
+      a.part_ml[(bh * nparts + part) * 2] = st.m;
+      a.part_ml[(bh * nparts + part) * 2 + 1] = l;
+    }
+  }
+}
+
 // Waves per decode workgroup (each wave has private LDS tiles).
 template <int D> struct DecodeWaves { static constexpr int N = D == 256 ? 2 : 4; };
 
@@ -757,13 +911,15 @@ __device__ void decode_impl(const FaArgs& a) {
   }
 }
 
+#define MXFA_DECODE_SPLIT(D, SC, NAME)                                                 \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC>(a); }
 #define MXFA_DECODE(D, SC, NAME)                                                       \
   extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<D>::N) NAME(FaArgs a) { decode_impl<D, SC>(a); }
-MXFA_DECODE(64, false, mxfa_decode_d64)
-MXFA_DECODE(128, false, mxfa_decode_d128)
+MXFA_DECODE_SPLIT(64, false, mxfa_decode_d64)
+MXFA_DECODE_SPLIT(128, false, mxfa_decode_d128)
 MXFA_DECODE(256, false, mxfa_decode_d256)
-MXFA_DECODE(64, true, mxfa_decode_d64_softcap)
-MXFA_DECODE(128, true, mxfa_decode_d128_softcap)
+MXFA_DECODE_SPLIT(64, true, mxfa_decode_d64_softcap)
+MXFA_DECODE_SPLIT(128, true, mxfa_decode_d128_softcap)
 MXFA_DECODE(256, true, mxfa_decode_d256_softcap)
 
 // Merge nparts partials per (b, query head) in part order: O = sum_i O_i 2^{(m_i - M) c} / sum_i l_i 2^{(m_i - M) c}.
