@@ -63,20 +63,50 @@ def time_calls(torch, fn, steps, warmup):
     return ev0.elapsed_time(ev1) / steps
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_hbm_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per prefill launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE, each scaled by its plain-copy calibration factor), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy(torch):
+    """A plain device-to-device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
+    counters (run under rocprofv3 --pmc)."""
+    n = 256 * 1024 * 1024
+    a = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_per_copy": n, "copies": 3}), flush=True)
+
+
 def cpu_baseline(mxfa, p, ops_host, threads):
-    """The CPU oracle (this repo's C restatement, threaded) on a bounded sample of the
-    same workload: batch 0, query heads 0-3 (one KV group) = 1/16 of configs[2]."""
+    """The CPU oracle (this repo's C restatement of the reference algorithm, threaded over
+    query heads) on the whole configs[2] workload: every (batch, query head), the same
+    block size.  About 40 thread-seconds of CPU work on 16 threads."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     op = O.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim,
                        causal=bool(p.causal), scale=p.softmax_scale)
-    heads = [0, 1, 2, 3]
     t0 = time.time()
-    O.attention(op, *ops_host, block_n=mxfa.DEFAULT_BLOCK_N, heads=heads, nthreads=threads)
+    O.attention(op, *ops_host, block_n=mxfa.DEFAULT_BLOCK_N, nthreads=threads)
     dt = time.time() - t0
-    flops = 4.0 * p.head_dim * len(heads) * mxfa.visible_pairs(p)
+    flops = mxfa.attention_flops(p)
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"batch 0, query heads 0-3 of configs[2] ({flops / 1e9:.1f} GFLOP, {dt:.2f} s wall)"}
+            "sample": f"all of configs[2]: {p.batch} x {p.num_q_heads} query heads ({flops / 1e9:.1f} GFLOP, "
+                      f"{dt:.2f} s wall on {threads} threads)"}
 
 
 def main():
@@ -86,6 +116,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true", help="only run a 256 MiB device copy x3")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in DESIGN.md)",
@@ -93,8 +124,11 @@ def main():
         sys.exit(2)
 
     import torch
-    import mxfa
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
+    import mxfa
     mxfa.init()
 
     c = prefill_config()
@@ -122,7 +156,7 @@ def main():
                    "causal": True, "block_n": mxfa.DEFAULT_BLOCK_N, "gflop_per_step": round(flops / 1e9, 2)},
         "pct_mxfp8_peak": round(100.0 * tflops / MXFP8_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic()},
     }
 
     if not args.no_decode:

@@ -13,6 +13,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -170,9 +171,24 @@ const char* kernel_name(const char* kind, int D, bool softcap) {
 
 // Decode geometry: chunks of split_len keys (multiple of 64) so that the whole
 // call has about 16K waves in flight.
+// Split-KV plan: chunks of split_len keys (a multiple of 64) so that about kDecodeWaves
+// chunk waves cover the cache -- about 1.5 waves per decode wave slot of the 256-CU chip
+// (8 per CU): one round of long chunks, few partials to merge (measured on MI355X:
+// 16384 waves 4.7 TB/s, 2048 5.3, 1536 5.4).  MXFA_DECODE_WAVES overrides the target.
+constexpr int64_t kDecodeWaves = 1536;
+
+int64_t decode_wave_target() {
+  if (const char* env = getenv("MXFA_DECODE_WAVES")) {
+    long long v = atoll(env);
+    if (v > 0) return v;
+  }
+  return kDecodeWaves;
+}
+
 void decode_geometry(const mxfa_attn_params* p, int* split_len, int* nparts) {
   int64_t bk = (int64_t)p->batch * p->num_kv_heads;
-  int64_t target = (16384 + bk - 1) / bk;
+  const int64_t waves = decode_wave_target();
+  int64_t target = (waves + bk - 1) / bk;
   if (target < 1) target = 1;
   int64_t len = (p->seq_k + target - 1) / target;
   len = (len + 63) / 64 * 64;
