@@ -92,6 +92,35 @@ def calibrate_copy(torch):
     print(json.dumps({"calibration": "device copy", "bytes_per_copy": n, "copies": 3}), flush=True)
 
 
+def bench_kv_append(torch, mxfa, args):
+    """KV-cache append (mxfa_kv_append): a 4096-token prefill chunk into a configs[2]-shape
+    cache (B=2, Hkv=8, D=128) and a one-token decode step into a configs[4]-shape cache
+    (B=64, Hkv=8, D=128, position 8191, whose open V block is re-quantized from the fp32
+    tail).  Bytes = fp32 tokens read + codes/scales written + tail read/written."""
+    dev = "cuda:0"
+    out = {}
+    for name, (B, H, D, L, pos, n) in {"prefill_4096": (2, 8, 128, 4096, 0, 4096),
+                                       "decode_step": (64, 8, 128, 8192, 8191, 1)}.items():
+        cache = mxfa.KvCache(B, H, D, L)
+        kn = torch.empty((B, H, n, D), dtype=torch.float32, device=dev)
+        vn = torch.empty_like(kn)
+        mxfa.fill_normal(kn, 21)
+        mxfa.fill_normal(vn, 22)
+
+        def call():
+            cache.length = pos
+            cache.append(kn, vn)
+        ms = time_calls(torch, call, args.steps, args.warmup)
+        tok_in = 2 * B * H * n * D * 4
+        blocks = (pos + n - 1) // 32 - pos // 32 + 1
+        codes = B * H * (n * D + n * D // 32 + blocks * 32 * D + blocks * D)
+        tail = B * H * 32 * D * 4 * ((1 if pos % 32 else 0) + (1 if (pos + n) % 32 else 0))   # read + write
+        nbytes = tok_in + codes + tail
+        out[name] = {"workload": f"B={B} Hkv={H} D={D}, {n} token(s) at position {pos}", "ms_per_call": round(ms, 4),
+                     "bytes_per_call": nbytes, "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}
+    return out
+
+
 def cpu_baseline(mxfa, p, ops_host, threads):
     """The CPU oracle (this repo's C restatement of the reference algorithm, threaded over
     query heads) on the whole configs[2] workload: every (batch, query head), the same
@@ -182,6 +211,9 @@ def main():
         result["decode"] = {"workload": "configs[4]: decode B=64 Hq=32 Hkv=8 D=128 KV length 8192, E4M3 MX KV cache",
                             "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(msd, 4),
                             "bytes_per_call": nbytes, "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+    if not args.no_decode:
+        result["kv_append"] = bench_kv_append(torch, mxfa, args)
 
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)

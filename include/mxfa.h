@@ -107,6 +107,33 @@ mxfa_status mxfa_decode(const mxfa_attn_params *p,
                         const uint8_t *v_cache, const uint8_t *v_sc,
                         float *o, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- KV cache ---- */
+
+/* KV-cache shape for mxfa_kv_append: caches k [B][Hkv][max_len][D] + k_sc [B][Hkv][max_len][D/32],
+ * v [B][Hkv][max_len][D] + v_sc [B][Hkv][max_len/32][D] (the layouts mxfa_decode reads). */
+typedef struct {
+  int32_t batch, num_kv_heads;
+  int32_t head_dim;                         /* multiple of 32                                 */
+  int32_t max_len;                          /* cache capacity in tokens, multiple of 32       */
+  int32_t v_fmt;                            /* mxfa_fmt of V (K is E4M3)                      */
+} mxfa_kv_params;
+
+/* Append n_new tokens at positions pos0 .. pos0+n_new-1 of every (batch, KV head) to an
+ * MXFP8 KV cache with rule R1 (lib/golden/mx_golden.cpp:146-190): K rows per token
+ * (32-blocks along D); V in 32-token blocks along the sequence (the reference's
+ * V_scales[Sk/32][d], kernels/flash_attention_mx/gen_data.py:118-119).  The block still
+ * open after the append is kept in fp32 in v_tail [B][Hkv][32][D] (caller-owned, kept
+ * between calls) and re-quantized by the next append; positions not appended yet count
+ * as 0.  After any sequence of appends (each starting at 0 or where the previous one
+ * ended) the cache equals mxfa_quantize_rows / mxfa_quantize_cols of the whole sequence
+ * (zero-padded to its 32-token block), bit for bit.  k_new, v_new: [B][Hkv][n_new][D] fp32.
+ * Decode over L tokens: seq_k = L rounded up to 32, q_pos0 = L - 1 (the padding is masked
+ * causally).  The reference has no cache (its operands are baked into a header); this is the
+ * producer side of the decode path. */
+mxfa_status mxfa_kv_append(const mxfa_kv_params *p, const float *k_new, const float *v_new,
+                           int32_t pos0, int32_t n_new, uint8_t *k_cache, uint8_t *k_sc,
+                           uint8_t *v_cache, uint8_t *v_sc, float *v_tail, void *stream);
+
 /* The attention kernels' softmax-requant step on caller scores, exposed so that it can
  * be checked bit-exactly in isolation.  Replaces fused_softmax_requant
  * (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:315-394) with rule R1

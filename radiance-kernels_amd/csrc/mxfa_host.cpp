@@ -41,7 +41,8 @@ const char* const kKernelNames[] = {
     "mxfa_softmax_requant_rows",     "mxfa_fill_normal_f32",    "mxfa_prefill_d64",     "mxfa_prefill_d128",
     "mxfa_prefill_d256",       "mxfa_prefill_d64_softcap", "mxfa_prefill_d128_softcap", "mxfa_prefill_d256_softcap",
     "mxfa_decode_d64",         "mxfa_decode_d128",        "mxfa_decode_d256",     "mxfa_decode_d64_softcap",
-    "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine",
+    "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine", "mxfa_kv_append_e4m3",
+    "mxfa_kv_append_e3m2",     "mxfa_kv_tail_update",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -260,6 +261,47 @@ mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32
   dim3 grid((unsigned)((threads + 255) / 256));
   void* args[] = {(void*)&x, &mats, &rows, &cols, &codes, &scales};
   return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : "mxfa_quant_cols_e3m2", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_kv_append(const mxfa_kv_params* p, const float* k_new, const float* v_new, int32_t pos0, int32_t n_new,
+                           uint8_t* k_cache, uint8_t* k_sc, uint8_t* v_cache, uint8_t* v_sc, float* v_tail,
+                           void* stream) {
+  if (!p) return fail(MXFA_ERR_INVALID_ARG, "params is NULL");
+  if (p->batch < 1 || p->num_kv_heads < 1) return fail(MXFA_ERR_INVALID_ARG, "batch and num_kv_heads must be >= 1");
+  if (p->head_dim < 32 || p->head_dim % 32) return fail(MXFA_ERR_INVALID_ARG, "head_dim must be a positive multiple of 32");
+  if (p->max_len < 32 || p->max_len % 32) return fail(MXFA_ERR_INVALID_ARG, "max_len must be a positive multiple of 32");
+  if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad v_fmt");
+  if (pos0 < 0 || n_new < 0 || (int64_t)pos0 + n_new > p->max_len)
+    return fail(MXFA_ERR_INVALID_ARG, "need 0 <= pos0 and pos0 + n_new <= max_len");
+  if (n_new == 0) return MXFA_OK;
+  const void* ptrs[] = {k_new, v_new, k_cache, k_sc, v_cache, v_sc, v_tail};
+  for (const void* q : ptrs)
+    if (!q) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  for (const void* q : ptrs)
+    if (!aligned16(q)) return fail(MXFA_ERR_INVALID_ARG, "buffers must be 16-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  const int64_t bk = (int64_t)p->batch * p->num_kv_heads;
+  int D = p->head_dim, L = p->max_len, n = n_new, pos = pos0;
+  // one launch: K (8 lanes per 32-block) then V (one wave per 32 columns of a touched
+  // 32-token block)
+  int64_t kblocks = bk * n * (D / 32);
+  int kgroups = (int)((kblocks * 8 + 255) / 256);
+  const int end = pos0 + n_new;
+  int ntouch = (end - 1) / 32 - pos0 / 32 + 1;
+  int64_t vunits = bk * ntouch * (D / 32);
+  const int64_t vgroups = (vunits + 3) / 4;
+  if (kgroups + vgroups > 0x7fffffffLL) return fail(MXFA_ERR_UNSUPPORTED, "append too large for one launch");
+  void* args[] = {(void*)&k_new, (void*)&v_new, &v_tail, &kblocks, &kgroups, &vunits, &ntouch,
+                  &n, &L, &D, &pos, &k_cache, &k_sc, &v_cache, &v_sc};
+  if (mxfa_status st = launch(dm, p->v_fmt == MXFA_FMT_E4M3 ? "mxfa_kv_append_e4m3" : "mxfa_kv_append_e3m2",
+                              dim3((unsigned)(kgroups + vgroups)), dim3(256), args, stream))
+    return st;
+  if (end % 32 == 0 || ntouch == 1) return MXFA_OK;   // no open block, or its tail is already written
+  // the block left open after a multi-block append keeps its fp32 values for the next one
+  int64_t tthreads = bk * 32 * (D / 4);
+  void* ta[] = {(void*)&v_new, &v_tail, &tthreads, &n, &D, &pos};
+  return launch(dm, "mxfa_kv_tail_update", dim3((unsigned)((tthreads + 255) / 256)), dim3(256), ta, stream);
 }
 
 mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, int64_t rows, int32_t cols,

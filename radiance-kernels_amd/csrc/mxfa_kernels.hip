@@ -141,6 +141,139 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e3m2(const flo
 }
 
 // ============================================================================
+// KV-cache append (rule R1).  K: each new token's row is quantized into cache row
+// pos0 + i (32-blocks along D).  V: every 32-token block touched by the append is
+// re-quantized as a whole from the open block's fp32 tail (positions before pos0), the new
+// tokens, and zeros for positions not appended yet (zeros leave R1's amax unchanged), so
+// the cache always equals the R1 quantization of the sequence so far.  The block left
+// open keeps its fp32 values in the tail: written by the same threads when the append
+// touches one block (each lane rewrites only the tail rows and columns it read), by a
+// second, stream-ordered kernel when it spans several (the old tail rows are read by the
+// first block's threads, the new ones belong to the last block).
+// One launch: workgroups [0, kgroups) do K, the rest V.
+// ============================================================================
+__device__ __forceinline__ void kv_append_k_part(const float* k_new, int64_t gt, int64_t nblocks, int n_new, int L,
+                                                 int D, int pos0, uint8_t* k_cache, uint8_t* k_sc) {
+  const int64_t blk = gt >> 3;
+  const int part = (int)(gt & 7);
+  if (blk >= nblocks) return;                       // whole 8-lane groups leave together
+  const int bpr = D / 32;
+  const int64_t row = blk / bpr;                    // (b * Hkv + kvh) * n_new + i
+  const int cb = (int)(blk % bpr);
+  const int64_t bk = row / n_new;
+  const int i = (int)(row % n_new);
+  const float4 v = reinterpret_cast<const float4*>(k_new + row * D + cb * 32)[part];
+  float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  a = fmaxf(a, __shfl_xor(a, 4));
+  const uint32_t sc = scale_code(a, 8);
+  const int64_t crow = bk * L + pos0 + i;
+  reinterpret_cast<uint32_t*>(k_cache + crow * D + cb * 32)[part] = encode4<0>(v, 127 - (int)sc);
+  if (part == 0) k_sc[crow * bpr + cb] = (uint8_t)sc;
+}
+
+// V: 64-lane units, each = 8 column groups of 4 x 8 row lanes of 4 rows of one (b * Hkv + kvh,
+// touched block); lane = cgl + 8 * rl.  Units per (bk, block) = D / 32.
+template <int FMT>
+__device__ __forceinline__ void kv_append_v_part(const float* v_new, float* v_tail, int64_t unit, int64_t nunits,
+                                                 int lane, int ntouch, int n_new, int L, int D, int pos0,
+                                                 uint8_t* v_cache, uint8_t* v_sc) {
+  if (unit >= nunits) return;                       // whole waves leave together
+  const int upb = D / 32;
+  const int64_t bk = unit / ((int64_t)ntouch * upb);
+  const int rem = (int)(unit % ((int64_t)ntouch * upb));
+  const int jb = rem / upb;
+  const int cgl = lane & 7, rl = lane >> 3;
+  const int c4 = (rem % upb) * 32 + cgl * 4;
+  const int end = pos0 + n_new;
+  const int blk = pos0 / 32 + jb;
+  const int p0 = blk * 32;
+  const int tail0 = (pos0 / 32) * 32;               // first position held by the tail
+  float4 x[4];
+  float4 amax = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int p = p0 + 4 * rl + i;
+    if (p < pos0)
+      x[i] = *reinterpret_cast<const float4*>(v_tail + (bk * 32 + (p - tail0)) * D + c4);
+    else if (p < end)
+      x[i] = *reinterpret_cast<const float4*>(v_new + (bk * n_new + (p - pos0)) * D + c4);
+    else
+      x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    amax.x = fmaxf(amax.x, fabsf(x[i].x)); amax.y = fmaxf(amax.y, fabsf(x[i].y));
+    amax.z = fmaxf(amax.z, fabsf(x[i].z)); amax.w = fmaxf(amax.w, fabsf(x[i].w));
+  }
+#pragma unroll
+  for (int m = 8; m < 64; m <<= 1) {
+    amax.x = fmaxf(amax.x, __shfl_xor(amax.x, m)); amax.y = fmaxf(amax.y, __shfl_xor(amax.y, m));
+    amax.z = fmaxf(amax.z, __shfl_xor(amax.z, m)); amax.w = fmaxf(amax.w, __shfl_xor(amax.w, m));
+  }
+  const int lp = FMT == 0 ? 8 : 4;
+  const uint32_t s0 = scale_code(amax.x, lp), s1 = scale_code(amax.y, lp), s2 = scale_code(amax.z, lp),
+                 s3 = scale_code(amax.w, lp);
+  const bool tail_here = ntouch == 1 && (end % 32) != 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 4 * rl + i;
+    const float y0 = __builtin_ldexpf(x[i].x, 127 - (int)s0), y1 = __builtin_ldexpf(x[i].y, 127 - (int)s1);
+    const float y2 = __builtin_ldexpf(x[i].z, 127 - (int)s2), y3 = __builtin_ldexpf(x[i].w, 127 - (int)s3);
+    uint32_t w;
+    if (FMT == 0)
+      w = e4m3_code(y0) | (e4m3_code(y1) << 8) | (e4m3_code(y2) << 16) | (e4m3_code(y3) << 24);
+    else
+      w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
+          (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);
+    *reinterpret_cast<uint32_t*>(v_cache + (bk * L + p0 + r) * D + c4) = w;
+    if (tail_here && p0 + r >= pos0) *reinterpret_cast<float4*>(v_tail + (bk * 32 + r) * D + c4) = x[i];
+  }
+  if (rl == 0)
+    *reinterpret_cast<uint32_t*>(v_sc + (bk * (L / 32) + blk) * D + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
+}
+
+template <int FMT>
+__device__ void kv_append_impl(const float* k_new, const float* v_new, float* v_tail, int64_t kblocks, int kgroups,
+                               int64_t vunits, int ntouch, int n_new, int L, int D, int pos0, uint8_t* k_cache,
+                               uint8_t* k_sc, uint8_t* v_cache, uint8_t* v_sc) {
+  if ((int)blockIdx.x < kgroups) {
+    kv_append_k_part((const float*)k_new, (int64_t)blockIdx.x * blockDim.x + threadIdx.x, kblocks, n_new, L, D, pos0,
+                     k_cache, k_sc);
+  } else {
+    const int64_t unit = ((int64_t)blockIdx.x - kgroups) * (blockDim.x / 64) + (threadIdx.x >> 6);
+    kv_append_v_part<FMT>(v_new, v_tail, unit, vunits, threadIdx.x & 63, ntouch, n_new, L, D, pos0, v_cache, v_sc);
+  }
+}
+
+#define MXFA_KV_APPEND(FMT, NAME)                                                                             \
+  extern "C" __global__ void __launch_bounds__(256)                                                          \
+      NAME(const float* k_new, const float* v_new, float* v_tail, int64_t kblocks, int kgroups, int64_t vunits, \
+           int ntouch, int n_new, int L, int D, int pos0, uint8_t* k_cache, uint8_t* k_sc, uint8_t* v_cache,   \
+           uint8_t* v_sc) {                                                                                    \
+    kv_append_impl<FMT>(k_new, v_new, v_tail, kblocks, kgroups, vunits, ntouch, n_new, L, D, pos0, k_cache, k_sc, \
+                        v_cache, v_sc);                                                                        \
+  }
+MXFA_KV_APPEND(0, mxfa_kv_append_e4m3)
+MXFA_KV_APPEND(1, mxfa_kv_append_e3m2)
+
+// Tail of the block left open by an append that spans several blocks: rows of positions
+// pos0 .. end - 1 from the new tokens, rows past the end zeroed (the block starts after
+// pos0, so it holds no earlier rows).  One thread per (b * Hkv + kvh, row, 4 columns).
+extern "C" __global__ void __launch_bounds__(256) mxfa_kv_tail_update(const float* v_new, float* v_tail,
+                                                                      int64_t nthreads, int n_new, int D, int pos0) {
+  const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gt >= nthreads) return;
+  const int cg = D / 4;
+  const int64_t bk = gt / (32 * cg);
+  const int rem = (int)(gt % (32 * cg));
+  const int r = rem / cg, c4 = (rem % cg) * 4;
+  const int end = pos0 + n_new;
+  const int p = ((end - 1) / 32) * 32 + r;
+  const float4 x = p < end ? *reinterpret_cast<const float4*>(v_new + (bk * n_new + (p - pos0)) * D + c4)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+  *reinterpret_cast<float4*>(v_tail + (bk * 32 + r) * D + c4) = x;
+}
+
+// ============================================================================
 // Synthetic inputs: x[i] ~ N(0,1) from a counter-based hash (splitmix64) and
 // Box-Muller; each element independently multiplied by `mul` with probability p.
 // ============================================================================

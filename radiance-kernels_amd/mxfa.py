@@ -12,6 +12,7 @@ vocabulary on top of the C ABI:
     prefill           -> mx_attention_flash[_causal_gqa | _gemma]
     decode            -> the same recurrence over an MXFP8 KV cache (split-KV)
     softmax_requant   -> fused_softmax_requant (the P tile step, for bit-exact checks)
+    KvCache.append    -> the producer side of decode: new tokens into the MXFP8 cache
 
 torch is used only to hold device memory and name the stream; every call goes through
 ctypes into libmxfa.so, which launches gfx950 kernels.  There is no fallback: if the
@@ -55,8 +56,13 @@ def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=N
                       int(block_n))
 
 
+class KvParams(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("max_len", ctypes.c_int32), ("v_fmt", ctypes.c_int32)]
+
+
 EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
-           "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
+           "mxfa_kv_append", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
            "mxfa_last_error", "mxfa_version")
 
 _lib = None
@@ -79,12 +85,13 @@ def lib():
         L.mxfa_softmax_requant.argtypes = [f32p, f32p, ctypes.c_float, ctypes.c_int64, ctypes.c_int32, f32p,
                                            u8p, u8p, f32p, vp]
         L.mxfa_fill_normal.argtypes = [f32p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp]
+        L.mxfa_kv_append.argtypes = [P(KvParams), f32p, f32p, ctypes.c_int32, ctypes.c_int32] + [u8p] * 4 + [f32p, vp]
         L.mxfa_status_string.argtypes = [ctypes.c_int]
         L.mxfa_status_string.restype = ctypes.c_char_p
         L.mxfa_last_error.restype = ctypes.c_char_p
         L.mxfa_version.restype = ctypes.c_int32
         for name in ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
-                     "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init"):
+                     "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_kv_append"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -189,6 +196,33 @@ def decode(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):
     _check(lib().mxfa_decode(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
                              _ptr(workspace), workspace.numel(), _stream(stream)))
     return out
+
+
+class KvCache:
+    """An MXFP8 KV cache on the device (the layouts decode reads) plus the fp32 tail of
+    its open V block; append() quantizes new tokens into it (mxfa_kv_append)."""
+
+    def __init__(self, batch, num_kv_heads, head_dim, max_len, v_fmt=FMT_E4M3, device="cuda:0"):
+        import torch
+        B, H, D, L = batch, num_kv_heads, head_dim, max_len
+        self.params = KvParams(B, H, D, L, v_fmt)
+        self.k = torch.zeros((B, H, L, D), dtype=torch.uint8, device=device)
+        self.ks = torch.zeros((B, H, L, D // 32), dtype=torch.uint8, device=device)
+        self.v = torch.zeros((B, H, L, D), dtype=torch.uint8, device=device)
+        self.vs = torch.zeros((B, H, L // 32, D), dtype=torch.uint8, device=device)
+        self.tail = torch.zeros((B, H, 32, D), dtype=torch.float32, device=device)
+        self.length = 0
+
+    def append(self, k_new, v_new, stream=None):
+        """k_new, v_new: contiguous float32 [B, Hkv, n_new, D] CUDA tensors."""
+        import torch
+        for t in (k_new, v_new):
+            assert t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.dim() == 4
+        n = k_new.shape[2]
+        _check(lib().mxfa_kv_append(ctypes.byref(self.params), _ptr(k_new), _ptr(v_new), self.length, n,
+                                    _ptr(self.k), _ptr(self.ks), _ptr(self.v), _ptr(self.vs), _ptr(self.tail),
+                                    _stream(stream)))
+        self.length += n
 
 
 def attention_flops(p):

@@ -100,3 +100,17 @@ def test_quantize_argument_validation():
     assert L.mxfa_softmax_requant(None, None, 1.0, 4, 33, None, None, None, None, None) == 1
     assert L.mxfa_softmax_requant(None, None, 0.0, 4, 32, None, None, None, None, None) == 1
     assert L.mxfa_softmax_requant(None, None, 1.0, 0, 32, None, None, None, None, None) == 0
+
+
+def test_kv_append_argument_validation():
+    L = mxfa.lib()
+    P = mxfa.KvParams
+    ok = P(2, 2, 128, 256, mxfa.FMT_E4M3)
+    z = [None] * 6
+    assert L.mxfa_kv_append(None, None, None, 0, 1, *z) == 1                       # no params
+    assert L.mxfa_kv_append(ctypes.byref(ok), None, None, 0, 0, *z) == 0           # nothing to append
+    assert L.mxfa_kv_append(ctypes.byref(ok), None, None, 0, 1, *z) == 1           # NULL buffers
+    assert L.mxfa_kv_append(ctypes.byref(ok), None, None, 250, 7, *z) == 1         # past max_len
+    assert L.mxfa_kv_append(ctypes.byref(ok), None, None, -1, 1, *z) == 1
+    for bad in (P(2, 2, 100, 256, 0), P(2, 2, 128, 250, 0), P(0, 2, 128, 256, 0), P(2, 2, 128, 256, 7)):
+        assert L.mxfa_kv_append(ctypes.byref(bad), None, None, 0, 1, *z) == 1

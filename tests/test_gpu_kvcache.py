@@ -1,0 +1,86 @@
+"""GPU parity of the KV-cache append (mxfa_kv_append): after every append of a ragged
+sequence of chunks, the cache equals the oracle's one-shot R1 quantization of everything
+appended so far (K rows; V in 32-token blocks, zero-padded) bit for bit, and decode over
+the appended cache matches the oracle."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import mxfa  # noqa: E402
+import oracle as O  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, np_, oracle_params  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def expected_cache(Kf, Vf, n, fmt):
+    """Oracle: K rows [.., :n, :] and V blocks of the zero-padded first n tokens."""
+    B, H, _, D = Kf.shape
+    n32 = -(-n // 32) * 32
+    kc, ks = O.quantize_rows(np.ascontiguousarray(Kf[:, :, :n]).reshape(-1, D), O.FMT_E4M3)
+    Vp = np.zeros((B, H, n32, D), np.float32)
+    Vp[:, :, :n] = Vf[:, :, :n]
+    vc, vs = O.quantize_cols(Vp, fmt)
+    return kc.reshape(B, H, n, D), ks.reshape(B, H, n, D // 32), vc, vs
+
+
+@pytest.mark.parametrize("D,fmt", [(128, mxfa.FMT_E4M3), (64, mxfa.FMT_E3M2), (256, mxfa.FMT_E4M3)])
+def test_append_matches_one_shot_quantization(D, fmt):
+    B, H, L = 2, 3, 320
+    rng = np.random.default_rng(400 + D)
+    Kf = (rng.standard_normal((B, H, L, D)) * 2.0 ** rng.integers(-6, 6, (1, 1, L, 1))).astype(np.float32)
+    Vf = (rng.standard_normal((B, H, L, D)) * 2.0 ** rng.integers(-6, 6, (1, 1, L, 1))).astype(np.float32)
+    Vf[:, :, 40:44] = 0.0                                            # all-zero rows inside a block
+    cache = mxfa.KvCache(B, H, D, L, v_fmt=fmt)
+    sentinel = 0xA5
+    for t in (cache.k, cache.ks, cache.v, cache.vs):
+        t.fill_(sentinel)
+    chunks = [1, 5, 26, 32, 7, 33, 64, 1, 1, 30, 45, 75]             # 320 tokens: starts mid-block, spans blocks
+    assert sum(chunks) == L
+    Kd, Vd = torch.from_numpy(Kf).to(DEV), torch.from_numpy(Vf).to(DEV)
+    for n in chunks:
+        p0 = cache.length
+        cache.append(Kd[:, :, p0:p0 + n].contiguous(), Vd[:, :, p0:p0 + n].contiguous())
+        torch.cuda.synchronize()
+        m = cache.length
+        m32 = -(-m // 32) * 32
+        kc, ks, vc, vs = expected_cache(Kf, Vf, m, fmt)
+        np.testing.assert_array_equal(np_(cache.k)[:, :, :m], kc)
+        np.testing.assert_array_equal(np_(cache.ks)[:, :, :m], ks)
+        np.testing.assert_array_equal(np_(cache.v)[:, :, :m32], vc)
+        np.testing.assert_array_equal(np_(cache.vs)[:, :, :m32 // 32], vs)
+        if m < L:                                                     # nothing past the block is written
+            assert np.all(np_(cache.k)[:, :, m:] == sentinel)
+            assert np.all(np_(cache.v)[:, :, m32:] == sentinel)
+
+
+def test_decode_over_appended_cache():
+    """Decode at a length that is not a multiple of 32 (seq_k rounded up, q_pos0 = L - 1
+    masks the padding), cache built by appends, against the oracle on that cache."""
+    B, Hq, Hkv, D, Lcap = 4, 8, 2, 128, 512
+    n = 389
+    rng = np.random.default_rng(410)
+    Kf = rng.standard_normal((B, Hkv, Lcap, D)).astype(np.float32)
+    Vf = rng.standard_normal((B, Hkv, Lcap, D)).astype(np.float32)
+    cache = mxfa.KvCache(B, Hkv, D, Lcap)
+    Kd, Vd = torch.from_numpy(Kf).to(DEV), torch.from_numpy(Vf).to(DEV)
+    for c in (100, 1, 131, 157):
+        p0 = cache.length
+        cache.append(Kd[:, :, p0:p0 + c].contiguous(), Vd[:, :, p0:p0 + c].contiguous())
+    assert cache.length == n
+    Q = torch.empty((B, Hq, 1, D), dtype=torch.float32, device=DEV)
+    mxfa.fill_normal(Q, 411)
+    q, qs = mxfa.quantize_rows(Q)
+    sk = -(-n // 32) * 32
+    p = mxfa.make_params(B, Hq, Hkv, 1, sk, D, causal=True, q_pos0=n - 1)
+    k, ks = cache.k[:, :, :sk].contiguous(), cache.ks[:, :, :sk].contiguous()
+    v, vs = cache.v[:, :, :sk].contiguous(), cache.vs[:, :, :sk // 32].contiguous()
+    o = mxfa.decode(p, q, qs, k, ks, v, vs)
+    torch.cuda.synchronize()
+    split_len, _ = mxfa.decode_plan(p)
+    want = O.attention(oracle_params(p), np_(q), np_(qs), np_(k), np_(ks), np_(v), np_(vs),
+                       block_n=mxfa.DEFAULT_BLOCK_N, split_len=split_len)
+    rel, mab = errors(np_(o), want)
+    print(f"   decode over appended cache: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
