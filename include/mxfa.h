@@ -78,6 +78,13 @@ typedef struct {
 mxfa_status mxfa_quantize_rows(const float *x, int64_t rows, int32_t cols, mxfa_fmt fmt,
                                uint8_t *codes, uint8_t *scales, void *stream);
 
+/* Rule R4, the reference's other software MX quantizer (kernels/simt_quant/kernel.cpp:43-117,
+ * golden lib/golden/golden.py:129-170): per 32-block of a row, e = ceil(log2(amax / 448)),
+ * E8M0 code clamp(e + 127, 0, 254), E4M3 elements round-half-even of x * 2^-e, saturating at
+ * 448, subnormals kept.  Same layouts as mxfa_quantize_rows (E4M3 only). */
+mxfa_status mxfa_quantize_rows_r4(const float *x, int64_t rows, int32_t cols,
+                                  uint8_t *codes, uint8_t *scales, void *stream);
+
 /* 32-blocks along the rows of each of `mats` rows x cols matrices (V, KV-cache V).
  * codes [mats][rows][cols], scales [mats][rows/32][cols]; rows % 32 == 0, cols % 4 == 0.
  * Replaces mx_quantize_cols(V.t()) of fa_gen_data.py:103-104. */

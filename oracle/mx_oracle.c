@@ -467,3 +467,84 @@ void orc_e4m3_encode_range(uint32_t bits_lo, uint32_t count, uint8_t *out) {
 void orc_e4m3_encode_array(const float *x, int64_t n, uint8_t *out) {
   for (int64_t i = 0; i < n; i++) out[i] = orc_e4m3_encode(x[i]);
 }
+
+/* ------------------------------------------------------------------------------------
+ * Rule R4: the reference's SIMT block quantizer (kernels/simt_quant/kernel.cpp:43-117,
+ * numpy golden lib/golden/golden.py:129-170).  Block scale e = ceil(log2(amax / 448))
+ * from amax's bits: e = (E - 127 - 8) + (mantissa > 0x600000), code clamp(e + 127, 0, 254),
+ * amax == 0 -> code 0 and multiplier 1; elements x * 2^-e (fp32 multiply, 2^-e built
+ * from bits (127 - e) << 23 as a 32-bit word, as the reference does) encoded with
+ * round-half-even, saturation at 448 and E4M3 subnormals kept (grid 2^-9).
+ * ------------------------------------------------------------------------------------ */
+static uint32_t r4_round_shift(uint32_t v, int sh) {   /* RNE of v / 2^sh, sh > 0 */
+  if (sh >= 32) return 0u;
+  uint32_t low = v & ((1u << sh) - 1u), half = 1u << (sh - 1), q = v >> sh;
+  return q + ((low > half || (low == half && (q & 1u))) ? 1u : 0u);
+}
+
+uint8_t orc_r4_encode(float y) {                     /* kernel.cpp:56-81 */
+  uint32_t x = f2u(y), s = ((x >> 31) & 1u) << 7, a = x & 0x7fffffffu;
+  if (a == 0u) return (uint8_t)s;
+  if (u2f(a) >= 448.0f) return (uint8_t)(s | 0x7eu);
+  int e = (int)((a >> 23) & 0xffu) - 127;
+  uint32_t sig = (1u << 23) | (a & 0x7fffffu);
+  if (e < -6) {
+    uint32_t q = r4_round_shift(sig, 14 - e);          /* value / 2^-9 */
+    return (uint8_t)(s | (q >= 8u ? (8u | (q - 8u)) : q));
+  }
+  uint32_t r = r4_round_shift(sig, 20);
+  int E = e;
+  if (r == 16u) { r = 8u; E++; }
+  int ef = E + 7;
+  uint32_t m = r - 8u;
+  if (ef > 15 || (ef == 15 && m == 7u)) return (uint8_t)(s | 0x7eu);
+  return (uint8_t)(s | ((uint32_t)ef << 3) | m);
+}
+
+uint8_t orc_r4_quantize_block(const float *v, uint8_t *codes) {   /* kernel.cpp:96-117 */
+  float amax = 0.0f;
+  for (int j = 0; j < 32; j++) {
+    float av = u2f(f2u(v[j]) & 0x7fffffffu);
+    if (av > amax) amax = av;
+  }
+  float mul = 1.0f;
+  uint8_t sc = 0;
+  if (amax != 0.0f) {
+    uint32_t ab = f2u(amax);
+    int e = ((int)((ab >> 23) & 0xffu) - 127 - 8) + ((ab & 0x7fffffu) > 0x600000u ? 1 : 0);
+    int c = e + 127;
+    sc = (uint8_t)(c < 0 ? 0 : (c > 254 ? 254 : c));
+    mul = u2f((uint32_t)(127 - e) << 23);
+  }
+  for (int j = 0; j < 32; j++) codes[j] = orc_r4_encode(v[j] * mul);
+  return sc;
+}
+
+void orc_r4_quantize_rows(const float *x, int64_t rows, int64_t cols, uint8_t *codes, uint8_t *scales) {
+  int64_t nb = cols / 32;
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t b = 0; b < nb; b++)
+      scales[r * nb + b] = orc_r4_quantize_block(x + r * cols + b * 32, codes + r * cols + b * 32);
+}
+
+/* Self-checks of the R4 element rule (test infrastructure): over the float bit patterns
+ * [lo, hi), count values whose R4 code differs from (mode 0) the R1 code -- the rules
+ * coincide from 2^-6 up -- or (mode 1) round-half-even of |y| * 512 on the subnormal grid
+ * (exact in double: y * 512 is exact, the rounding is done on the integer and half). */
+int64_t orc_r4_check(uint32_t lo, uint32_t hi, int mode) {
+  int64_t bad = 0;
+  for (uint32_t b = lo; b < hi; b++) {
+    float y = u2f(b);
+    uint8_t c = orc_r4_encode(y);
+    uint8_t want;
+    if (mode == 0) {
+      want = orc_e4m3_encode(y);
+    } else {
+      double t = (double)fabsf(y) * 512.0, f = floor(t), d = t - f;
+      double q = (d > 0.5 || (d == 0.5 && fmod(f, 2.0) != 0.0)) ? f + 1.0 : f;
+      want = (uint8_t)(((b >> 31) << 7) | (q >= 8.0 ? (8u | (uint32_t)(q - 8.0)) : (uint32_t)q));
+    }
+    bad += c != want;
+  }
+  return bad;
+}

@@ -110,6 +110,12 @@ int64_t orc_check_log2_vs_libm(uint32_t lo, uint32_t hi);
 void    orc_e4m3_encode_range(uint32_t bits_lo, uint32_t count, uint8_t *out);
 void    orc_e4m3_encode_array(const float *x, int64_t n, uint8_t *out);   /* orc_e4m3_encode per element */
 
+/* Rule R4 (kernels/simt_quant/kernel.cpp:43-117, lib/golden/golden.py:129-170) */
+uint8_t orc_r4_encode(float y);
+uint8_t orc_r4_quantize_block(const float *v, uint8_t *codes);
+void    orc_r4_quantize_rows(const float *x, int64_t rows, int64_t cols, uint8_t *codes, uint8_t *scales);
+int64_t orc_r4_check(uint32_t lo, uint32_t hi, int mode);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,10 @@ def lib():
         L.orc_check_log2_vs_libm.restype = ctypes.c_int64
         L.orc_e4m3_encode_range.argtypes = [ctypes.c_uint32, ctypes.c_uint32, P(ctypes.c_uint8)]
         L.orc_e4m3_encode_array.argtypes = [f32p, ctypes.c_int64, u8p]
+        L.orc_r4_encode.argtypes = [ctypes.c_float]; L.orc_r4_encode.restype = ctypes.c_uint8
+        L.orc_r4_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, u8p, u8p]
+        L.orc_r4_check.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
+        L.orc_r4_check.restype = ctypes.c_int64
         _lib = L
     return _lib
 
@@ -113,6 +117,17 @@ def quantize_cols(x, fmt):
     sf = scales.reshape(mats, rows // 32, cols)
     for m in range(mats):
         lib().orc_quantize_cols(_f32(xf[m]), rows, cols, fmt, _u8(cf[m]), _u8(sf[m]))
+    return codes, scales
+
+
+def r4_quantize_rows(x):
+    """Rule R4 (the reference's SIMT block quantizer) over 32-blocks along the last axis."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    codes = np.empty(x.shape, np.uint8)
+    scales = np.empty(tuple(x.shape[:-1]) + (cols // 32,), np.uint8)
+    lib().orc_r4_quantize_rows(_f32(x), rows, cols, _u8(codes), _u8(scales))
     return codes, scales
 
 

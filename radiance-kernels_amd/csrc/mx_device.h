@@ -78,6 +78,48 @@ __device__ __forceinline__ uint32_t e4m3_code(float y) {
   return s | ((uint32_t)(E + 7) << 3) | (uint32_t)q;
 }
 
+// Rule R4, the reference's SIMT block quantizer (kernels/simt_quant/kernel.cpp:43-117):
+// E4M3 code of y with round-half-even, saturation at 448 and subnormals kept (2^-9 grid).
+__device__ __forceinline__ uint32_t r4_round_shift(uint32_t v, int sh) {   // RNE of v / 2^sh, sh > 0
+  if (sh >= 32) return 0u;
+  const uint32_t low = v & ((1u << sh) - 1u), half = 1u << (sh - 1), q = v >> sh;
+  return q + ((low > half || (low == half && (q & 1u))) ? 1u : 0u);
+}
+
+__device__ __forceinline__ uint32_t r4_e4m3_code(float y) {
+  const uint32_t x = __float_as_uint(y), s = ((x >> 31) & 1u) << 7, a = x & 0x7fffffffu;
+  if (a == 0u) return s;
+  if (__uint_as_float(a) >= 448.0f) return s | 0x7eu;
+  const int e = (int)((a >> 23) & 0xffu) - 127;
+  const uint32_t sig = (1u << 23) | (a & 0x7fffffu);
+  if (e < -6) {
+    const uint32_t q = r4_round_shift(sig, 14 - e);
+    return s | (q >= 8u ? (8u | (q - 8u)) : q);
+  }
+  uint32_t r = r4_round_shift(sig, 20);
+  int E = e;
+  if (r == 16u) { r = 8u; E++; }
+  const int ef = E + 7;
+  const uint32_t m = r - 8u;
+  if (ef > 15 || (ef == 15 && m == 7u)) return s | 0x7eu;
+  return s | ((uint32_t)ef << 3) | m;
+}
+
+// R4 block scale from amax's bits: e = ceil(log2(amax / 448)) = (E - 135) + (mantissa >
+// 0x600000); code clamp(e + 127, 0, 254); the element multiplier 2^-e is built from the
+// 32-bit word (127 - e) << 23 exactly as the reference builds it.  amax == 0: code 0, 1.
+__device__ __forceinline__ uint32_t r4_scale(float amax, float& mul) {
+  if (amax == 0.0f) {
+    mul = 1.0f;
+    return 0u;
+  }
+  const uint32_t ab = __float_as_uint(amax);
+  const int e = ((int)((ab >> 23) & 0xffu) - 135) + ((ab & 0x7fffffu) > 0x600000u ? 1 : 0);
+  mul = __uint_as_float((uint32_t)(127 - e) << 23);
+  const int c = e + 127;
+  return (uint32_t)(c < 0 ? 0 : (c > 254 ? 254 : c));
+}
+
 // lib/golden bf16 RNE (+-0 -> +0, tiny -> +0, NaN quieted).
 __device__ __forceinline__ uint32_t bf16_rne(float x) {
   if (x == 0.0f) return 0u;

@@ -42,7 +42,7 @@ const char* const kKernelNames[] = {
     "mxfa_prefill_d256",       "mxfa_prefill_d64_softcap", "mxfa_prefill_d128_softcap", "mxfa_prefill_d256_softcap",
     "mxfa_decode_d64",         "mxfa_decode_d128",        "mxfa_decode_d256",     "mxfa_decode_d64_softcap",
     "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine", "mxfa_kv_append_e4m3",
-    "mxfa_kv_append_e3m2",     "mxfa_kv_tail_update",
+    "mxfa_kv_append_e3m2",     "mxfa_kv_tail_update",     "mxfa_quant_rows_r4",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -244,6 +244,20 @@ mxfa_status mxfa_quantize_rows(const float* x, int64_t rows, int32_t cols, mxfa_
   dim3 grid((unsigned)((threads + 255) / 256));
   void* args[] = {(void*)&x, &nblocks, &codes, &scales};
   return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_rows_e4m3" : "mxfa_quant_rows_e3m2", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_quantize_rows_r4(const float* x, int64_t rows, int32_t cols, uint8_t* codes, uint8_t* scales,
+                                  void* stream) {
+  if (rows < 0 || cols <= 0 || cols % 32) return fail(MXFA_ERR_INVALID_ARG, "cols must be a positive multiple of 32");
+  if (rows == 0) return MXFA_OK;
+  if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
+    return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte and codes 4-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  int64_t nblocks = rows * (int64_t)cols / 32;
+  void* args[] = {(void*)&x, &nblocks, &codes, &scales};
+  return launch(dm, "mxfa_quant_rows_r4", dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), args, stream);
 }
 
 mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32_t cols, mxfa_fmt fmt, uint8_t* codes,

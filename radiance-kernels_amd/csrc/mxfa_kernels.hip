@@ -93,6 +93,27 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_e3m2(const flo
   quant_rows_impl<1>(x, nblocks, codes, scales);
 }
 
+// Rule R4 (the reference's SIMT block quantizer), 32-blocks along each row; amax is the
+// reference's running "if (|x| > amax)" maximum, which skips NaN like fmaxf.
+extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_r4(const float* x, int64_t nblocks, uint8_t* codes,
+                                                                     uint8_t* scales) {
+  const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t blk = gt >> 3;
+  const int part = (int)(gt & 7);
+  if (blk >= nblocks) return;                       // whole 8-lane groups leave together
+  const float4 v = reinterpret_cast<const float4*>(x)[blk * 8 + part];
+  float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  a = fmaxf(a, __shfl_xor(a, 4));
+  float mul;
+  const uint32_t sc = r4_scale(a, mul);
+  reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = r4_e4m3_code(v.x * mul) | (r4_e4m3_code(v.y * mul) << 8) |
+                                                       (r4_e4m3_code(v.z * mul) << 16) |
+                                                       (r4_e4m3_code(v.w * mul) << 24);
+  if (part == 0) scales[blk] = (uint8_t)sc;
+}
+
 // 32-blocks along rows (V layout): each lane owns 4 adjacent columns of one
 // 32-row block.  mats matrices of rows x cols; rows % 32 == 0, cols % 4 == 0.
 template <int FMT>

@@ -9,6 +9,7 @@ vocabulary on top of the C ABI:
     fill_normal       -> make_inputs / make_inputs_gqa (synthetic N(0,1) [+ outliers])
     quantize_rows     -> mx_quantize_cols on Q and K (32-blocks along D)
     quantize_cols     -> mx_quantize_cols(V.t()) (32-blocks along the key axis)
+    quantize_rows_r4  -> the simt_quant block quantizer (rule R4)
     prefill           -> mx_attention_flash[_causal_gqa | _gemma]
     decode            -> the same recurrence over an MXFP8 KV cache (split-KV)
     softmax_requant   -> fused_softmax_requant (the P tile step, for bit-exact checks)
@@ -61,7 +62,7 @@ class KvParams(ctypes.Structure):
                 ("max_len", ctypes.c_int32), ("v_fmt", ctypes.c_int32)]
 
 
-EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
+EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
            "mxfa_kv_append", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
            "mxfa_last_error", "mxfa_version")
 
@@ -79,6 +80,7 @@ def lib():
         P = ctypes.POINTER
         L.mxfa_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int, u8p, u8p, vp]
         L.mxfa_quantize_cols.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int, u8p, u8p, vp]
+        L.mxfa_quantize_rows_r4.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, u8p, u8p, vp]
         L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
         L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
         L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
@@ -90,7 +92,7 @@ def lib():
         L.mxfa_status_string.restype = ctypes.c_char_p
         L.mxfa_last_error.restype = ctypes.c_char_p
         L.mxfa_version.restype = ctypes.c_int32
-        for name in ("mxfa_quantize_rows", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
+        for name in ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
                      "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_kv_append"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
@@ -126,6 +128,18 @@ def quantize_rows(x, fmt=FMT_E4M3, stream=None):
     codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     scales = torch.empty(tuple(x.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=x.device)
     _check(lib().mxfa_quantize_rows(_ptr(x), rows, cols, fmt, _ptr(codes), _ptr(scales), _stream(stream)))
+    return codes, scales
+
+
+def quantize_rows_r4(x, stream=None):
+    """Rule R4 (the reference's simt_quant block quantizer), 32-blocks along the last axis."""
+    import torch
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty(tuple(x.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=x.device)
+    _check(lib().mxfa_quantize_rows_r4(_ptr(x), rows, cols, _ptr(codes), _ptr(scales), _stream(stream)))
     return codes, scales
 
 

@@ -114,3 +114,10 @@ def test_kv_append_argument_validation():
     assert L.mxfa_kv_append(ctypes.byref(ok), None, None, -1, 1, *z) == 1
     for bad in (P(2, 2, 100, 256, 0), P(2, 2, 128, 250, 0), P(0, 2, 128, 256, 0), P(2, 2, 128, 256, 7)):
         assert L.mxfa_kv_append(ctypes.byref(bad), None, None, 0, 1, *z) == 1
+
+
+def test_quantize_r4_argument_validation():
+    L = mxfa.lib()
+    assert L.mxfa_quantize_rows_r4(None, 4, 48, None, None, None) == 1
+    assert L.mxfa_quantize_rows_r4(None, 0, 64, None, None, None) == 0
+    assert L.mxfa_quantize_rows_r4(None, 4, 64, None, None, None) == 1

@@ -161,3 +161,25 @@ def test_fill_normal_statistics():
     z = torch.empty(1 << 10, dtype=torch.float32, device=DEV)
     mxfa.fill_normal(z, 7)
     np.testing.assert_array_equal(np_(z), a[:1 << 10].astype(np.float32))   # counter-based: prefix-stable
+
+
+def test_quantize_rows_r4_bit_exact():
+    """Rule R4 (the reference's simt_quant block quantizer) on the GPU vs the oracle:
+    random blocks over 60 binades, the edge rows of the R1 tests (amax around powers of
+    two, zeros, NaN, inf, 3e38, subnormals) and amax around 448 * 2^k."""
+    rng = np.random.default_rng(510)
+    e = edge_rows(rng)
+    e = e[: len(e) // 2 * 2].reshape(-1, 64)
+    t = []
+    for k in range(-130, 119, 5):
+        base = np.float32(448.0 * 2.0 ** k) if k > -120 else np.float32(2.0 ** k)
+        r = rng.standard_normal(64).astype(np.float32) * base / 4
+        r[0] = base
+        r[33] = np.nextafter(base, np.float32(np.inf))
+        t.append(r)
+    x = np.concatenate([e, np.stack(t), (rng.standard_normal((4096, 64)) * 2.0 ** rng.integers(-30, 30, (4096, 1))).astype(np.float32)])
+    codes, scales = mxfa.quantize_rows_r4(torch.from_numpy(np.ascontiguousarray(x)).to(DEV))
+    oc, osc = O.r4_quantize_rows(x)
+    np.testing.assert_array_equal(np_(scales), osc)
+    bad = np.argwhere(np_(codes) != oc)
+    assert len(bad) == 0, [(float(x[i, j]), int(np_(codes)[i, j]), int(oc[i, j])) for i, j in bad[:8]]

@@ -178,3 +178,57 @@ def test_quantize_rows_cols_roundtrip_error_bound():
     c2, s2 = O.quantize_cols(np.ascontiguousarray(x.T), O.FMT_E4M3)
     np.testing.assert_array_equal(c2, codes.T)
     np.testing.assert_array_equal(s2, scales.T)
+
+
+def _bits(x):
+    return int(np.array(x, np.float32).view(np.uint32))
+
+
+def test_r4_element_rule_equals_r1_from_2_pow_minus_6():
+    """Rule R4 (simt_quant) rounds and saturates like R1 wherever R1 does not flush: every
+    float in [2^-6, 2^10) of either sign gets the same E4M3 code, and a strided sample of
+    the saturating range above."""
+    L = O.lib()
+    lo, hi = _bits(2.0 ** -6), _bits(2.0 ** 10)                   # exhaustive up to 1024
+    assert L.orc_r4_check(lo, hi, 0) == 0
+    assert L.orc_r4_check(lo | 0x80000000, hi | 0x80000000, 0) == 0
+    for b in range(hi, 0x7F800000, 9973):                         # saturation region, sampled
+        assert L.orc_r4_check(b, b + 1, 0) == 0 and L.orc_r4_check(b | 0x80000000, (b | 0x80000000) + 1, 0) == 0
+
+
+def test_r4_element_rule_keeps_subnormals_on_the_2_pow_minus_9_grid():
+    """Below 2^-6 R4 keeps E4M3 subnormals: the code is round-half-even of |y| * 512
+    (checked over every float in [2^-24, 2^-6), both signs, and the smallest values)."""
+    L = O.lib()
+    lo, hi = _bits(2.0 ** -24), _bits(2.0 ** -6)
+    assert L.orc_r4_check(lo, hi, 1) == 0
+    assert L.orc_r4_check(lo | 0x80000000, hi | 0x80000000, 1) == 0
+    assert L.orc_r4_check(0, 4096, 1) == 0
+    assert L.orc_r4_encode(2.0 ** -10) == 0                    # tie -> even (0)
+    assert L.orc_r4_encode(3 * 2.0 ** -10) == 2                # tie -> even (2)
+    assert L.orc_r4_encode(7.75 * 2.0 ** -9) == 0x08           # rounds up to 2^-6, a normal code
+
+
+def test_r4_scale_is_ceil_log2_amax_over_448():
+    """R4's block scale: the smallest e with amax <= 448 * 2^e (exact in double), code
+    e + 127 clamped to [0, 254]; amax = 0 gives code 0.  Includes amax exactly at and just
+    around 448 * 2^k."""
+    rng = np.random.default_rng(500)
+    amaxes = list(np.exp2(rng.uniform(-118, 127, 4000)).astype(np.float32))
+    for k in range(-120, 120, 7):
+        t = np.float32(448.0 * 2.0 ** k)
+        amaxes += [t, np.nextafter(t, np.float32(0)), np.nextafter(t, np.float32(np.inf))]
+    amaxes = [a for a in amaxes if np.isfinite(a) and a >= np.float32(2.0 ** -126)]
+    x = np.zeros((len(amaxes), 32), np.float32)
+    x[:, 7] = -np.array(amaxes, np.float32)
+    x[:, 3] = np.array(amaxes, np.float32) * np.float32(0.25)
+    _, sc = O.r4_quantize_rows(x)
+    for a, s in zip(amaxes, sc[:, 0]):
+        e = int(np.ceil(np.log2(float(a) / 448.0)))
+        while 448.0 * 2.0 ** e < float(a):
+            e += 1
+        while 448.0 * 2.0 ** (e - 1) >= float(a):
+            e -= 1
+        assert s == min(max(e + 127, 0), 254), (a, s, e)
+    _, sc0 = O.r4_quantize_rows(np.zeros((1, 32), np.float32))
+    assert sc0[0, 0] == 0
