@@ -48,11 +48,23 @@ def make_prefill(torch, mxfa, c, seed=1):
     return p, (q, qs, k, ks, v, vs)
 
 
+PREHEAT_S = 0.25
+
+
 def time_calls(torch, fn, steps, warmup):
-    """Average ms per call with HIP events on the launch stream (torch's current stream)."""
+    """Average ms per call with HIP events on the launch stream (torch's current stream).
+    Untimed before the K timed calls: the W warmup calls, then more calls until at least
+    PREHEAT_S seconds of them have run -- the shader clock needs about that long under load
+    to settle (measured: a 10-call warmup of the prefill kernel left the timed calls ~12%
+    slower than steady state)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.time()
+    while time.time() - t0 < PREHEAT_S:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
@@ -141,8 +153,8 @@ def cpu_baseline(mxfa, p, ops_host, threads):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="only run a 256 MiB device copy x3")
@@ -174,6 +186,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "preheat_s": PREHEAT_S,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -187,6 +200,14 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic()},
     }
+
+    # the same workload with the reference device kernels' P rule (R2 compatibility mode)
+    p2 = mxfa.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim, causal=True,
+                          p_rule=mxfa.P_R2)
+    ms2 = time_calls(torch, lambda: mxfa.prefill(p2, *ops, out=out), args.steps, args.warmup)
+    result["prefill_p_rule_r2"] = {"workload": "configs[2] with P rule R2 (bf16 P, truncating target-0 requant)",
+                                   "value": round(flops / (ms2 * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                                   "ms_per_call": round(ms2, 4)}
 
     if not args.no_decode:
         dc = decode_config()

@@ -53,6 +53,16 @@ typedef enum {
 
 typedef enum { MXFA_FMT_E4M3 = 0, MXFA_FMT_E3M2 = 1 } mxfa_fmt;
 
+/* Requant rule of the probabilities P (the PV operand).
+ *  MXFA_P_R1: lib/golden's block-32 rule (lib/golden/mx_golden.cpp:146-190): scale
+ *             floor(log2f(amax)) - 8, E4M3 round-half-even saturating at 448.
+ *  MXFA_P_R2: the reference device kernels' "target-0" rule
+ *             (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:53-77, 366-388, 485-501):
+ *             P rounded to bf16, scale = exponent of the bf16 block max clamped to <= 0,
+ *             E4M3 by truncating the bf16 mantissa to 3 bits, flush below 2^(scale-6).
+ *             l then sums the bf16 P. */
+typedef enum { MXFA_P_R1 = 0, MXFA_P_R2 = 1 } mxfa_p_rule;
+
 /* Attention parameters (the reference's generated FA_* defines,
  * kernels/flash_attention_mx_gemma/fa_gen_data.py:147-181). */
 typedef struct {
@@ -66,6 +76,7 @@ typedef struct {
   float   softcap;                          /* FA_ATTN_SOFTCAP: 0 = off; s <- cap*tanh(s/cap) after scale */
   int32_t v_fmt;                            /* mxfa_fmt of V (Q and K are E4M3)                          */
   int32_t block_n;                          /* FA_BK: online-softmax key block; 0 = default (64)         */
+  int32_t p_rule;                           /* mxfa_p_rule of P; 0 = MXFA_P_R1                           */
 } mxfa_attn_params;
 
 /* ---- MX quantization (rule of lib/golden/mx_golden.cpp:146-190 with the element
@@ -143,16 +154,18 @@ mxfa_status mxfa_kv_append(const mxfa_kv_params *p, const float *k_new, const fl
 
 /* The attention kernels' softmax-requant step on caller scores, exposed so that it can
  * be checked bit-exactly in isolation.  Replaces fused_softmax_requant
- * (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:315-394) with rule R1
- * (lib/golden/mx_golden.cpp:146-190).  s [rows][cols] (cols % 32 == 0) are scores in the
- * units of c (P = 2^((s - row_max) * c)), row_max [rows] >= every score of its row.  Per
- * 32-block of a row: sc = R1 scale of amax = 2^((block max - row_max) * c) (exactly 1
- * where the block holds the row max), codes = R1 E4M3 codes of P * 2^(127 - sc).
- * Outputs p [rows][cols] (P as computed on the device), codes [rows][cols],
- * scales [rows][cols/32], row_sum [rows] = sum of P. */
+ * (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:315-394).  s [rows][cols]
+ * (cols % 32 == 0) are scores in the units of c (P = 2^((s - row_max) * c)), row_max
+ * [rows] >= every score of its row.  Per 32-block of a row, with amax = 2^((block max -
+ * row_max) * c) (exactly 1 where the block holds the row max):
+ *   MXFA_P_R1: sc = R1 scale of amax, codes = R1 E4M3 codes of P * 2^(127 - sc);
+ *   MXFA_P_R2: P rounded to bf16, sc = the bf16 exponent field of amax (<= 127), codes =
+ *              R2 codes of the bf16 P with se = sc - 127.
+ * Outputs p [rows][cols] (P as computed on the device, bf16-rounded under R2), codes
+ * [rows][cols], scales [rows][cols/32], row_sum [rows] = sum of p. */
 mxfa_status mxfa_softmax_requant(const float *s, const float *row_max, float c, int64_t rows,
-                                 int32_t cols, float *p, uint8_t *codes, uint8_t *scales,
-                                 float *row_sum, void *stream);
+                                 int32_t cols, int32_t p_rule, float *p, uint8_t *codes,
+                                 uint8_t *scales, float *row_sum, void *stream);
 
 /* Synthetic inputs: x[i] ~ N(0,1) (counter-based hash + Box-Muller), each element
  * multiplied by outlier_mul with probability outlier_p.  Replaces make_inputs /

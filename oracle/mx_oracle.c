@@ -287,18 +287,23 @@ static void flash_pass(const orc_attn_params *p, const double *qd, const double 
     double m_new = m > bmax ? m : bmax;
     if (m_new == -INFINITY) continue;               /* nothing visible yet */
     double corr = (m == -INFINITY) ? 0.0 : exp(m - m_new);
-    double lsum = 0.0;
-    for (int t = 0; t < n; t++) {
-      P[t] = S[t] == -INFINITY ? 0.0f : (float)exp(S[t] - m_new);
-      lsum += (double)P[t];
-    }
-    l = l * corr + lsum;
-    for (int d = 0; d < D; d++) O[d] *= corr;
-    /* requant P per 32-key group (global key index), rule R1 E4M3 */
+    for (int t = 0; t < n; t++) P[t] = S[t] == -INFINITY ? 0.0f : (float)exp(S[t] - m_new);
+    /* requant P per 32-key group (global key index): rule R1 E4M3, or rule R2 on the
+     * bf16-rounded P (which is then also the P summed into l) */
+    uint8_t gcodes[ORC_MAX_BLOCK_N], gsc[ORC_MAX_BLOCK_N / 32];
     for (int t = 0; t < n; t += 32) {
       int g = n - t < 32 ? n - t : 32;
-      uint8_t codes[32];
-      uint8_t sc = orc_quantize_block(P + t, 1, g, ORC_FMT_E4M3, codes, 1);
+      gsc[t / 32] = p->p_rule == ORC_P_R2 ? orc_r2_quantize_block(P + t, g, P + t, gcodes + t)
+                                          : orc_quantize_block(P + t, 1, g, ORC_FMT_E4M3, gcodes + t, 1);
+    }
+    double lsum = 0.0;
+    for (int t = 0; t < n; t++) lsum += (double)P[t];
+    l = l * corr + lsum;
+    for (int d = 0; d < D; d++) O[d] *= corr;
+    for (int t = 0; t < n; t += 32) {
+      int g = n - t < 32 ? n - t : 32;
+      const uint8_t *codes = gcodes + t;
+      uint8_t sc = gsc[t / 32];
       double scale = orc_e8m0_decode(sc);
       for (int u = 0; u < g; u++) {
         if (!codes[u]) continue;
@@ -395,7 +400,8 @@ static int run_attention(const orc_attn_params *p, const uint8_t *q, const uint8
       p->seq_k <= 0 || p->head_dim <= 0 || p->head_dim % 32 || p->seq_k % 32 ||
       p->num_q_heads % p->num_kv_heads)
     return -1;
-  if (!dense && (block_n <= 0 || block_n % 32)) return -1;
+  if (!dense && (block_n <= 0 || block_n % 32 || block_n > ORC_MAX_BLOCK_N)) return -1;
+  if (p->p_rule != ORC_P_R1 && p->p_rule != ORC_P_R2) return -1;
   if (split_len < 0 || (split_len > 0 && split_len % block_n)) return -1;
   int64_t nbh = (int64_t)p->batch * p->num_q_heads;
   int64_t nkv = (int64_t)p->batch * p->num_kv_heads;
@@ -547,4 +553,62 @@ int64_t orc_r4_check(uint32_t lo, uint32_t hi, int mode) {
     bad += c != want;
   }
   return bad;
+}
+
+/* ------------------------------------------------------------------------------------
+ * Rule R2: the reference device kernels' P requant ("target-0", truncating),
+ * kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:53-77 (bf16_floor_log2,
+ * bf16_to_e4m3_scaled) and :485-501 / :366-388 (per-block use).  P is bf16; the block
+ * exponent se is the unbiased exponent field of the bf16 block maximum, clamped to <= 0,
+ * so the maximum maps into [1, 2); scale code se + 127.  An element keeps its bf16
+ * exponent minus se and the top 3 bits of its bf16 mantissa (truncation), is flushed
+ * when its bf16 exponent field is 0 or the shifted exponent is below -6, and saturates
+ * to 448 (E = 8, m = 6) above.
+ * ------------------------------------------------------------------------------------ */
+uint8_t orc_r2_encode(uint16_t b, int se) {
+  int ex = (b >> 7) & 0xff;
+  int E = ex - 127 - se;
+  if (ex == 0 || E < -6) return 0;
+  int m3 = (b >> 4) & 7;
+  if (E > 8) {
+    E = 8;
+    m3 = 6;
+  } else if (E == 8 && m3 > 6) {
+    m3 = 6;
+  }
+  return (uint8_t)(((b >> 8) & 0x80) | ((E + 7) << 3) | m3);
+}
+
+int orc_r2_scale_exp(float amax) {
+  int se = (int)((orc_f32_to_bf16(amax) >> 7) & 0xff) - 127;
+  return se > 0 ? 0 : se;
+}
+
+/* One block of n <= 32 fp32 probabilities: P rounded to bf16 (written back to pb when
+ * non-NULL), scale from the bf16 block maximum, codes.  Returns the E8M0 code. */
+uint8_t orc_r2_quantize_block(const float *p, int n, float *pb, uint8_t *codes) {
+  uint16_t h[32];
+  float amax = 0.0f;
+  for (int i = 0; i < n; i++) {
+    h[i] = orc_f32_to_bf16(p[i]);
+    float v = u2f(((uint32_t)h[i] << 16) & 0x7fffffffu);
+    if (v > amax) amax = v;
+    if (pb) pb[i] = orc_bf16_to_f32(h[i]);
+  }
+  int se = orc_r2_scale_exp(amax);
+  for (int i = 0; i < n; i++) codes[i] = orc_r2_encode(h[i], se);
+  return (uint8_t)(se + 127);
+}
+
+void orc_r2_encode_array(const uint16_t *b, const int32_t *se, int64_t n, uint8_t *out) {
+  for (int64_t i = 0; i < n; i++) out[i] = orc_r2_encode(b[i], se[i]);
+}
+
+void orc_r2_quantize_rows(const float *p, int64_t rows, int64_t cols, float *pb, uint8_t *codes,
+                          uint8_t *scales) {
+  int64_t nb = cols / 32;
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t b = 0; b < nb; b++)
+      scales[r * nb + b] = orc_r2_quantize_block(p + r * cols + b * 32, 32, pb ? pb + r * cols + b * 32 : NULL,
+                                                 codes + r * cols + b * 32);
 }

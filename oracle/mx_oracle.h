@@ -25,7 +25,10 @@
  * (whose fp8_matmul_model dependency is not vendored): arithmetic is done in
  * double and P is rounded to fp32 before requantization, because the
  * MI355X kernels compute in fp32; the P requant rule is R1 (lib/golden),
- * which is the rule the build targets.
+ * which is the rule the build targets, or, with p_rule = ORC_P_R2, the
+ * reference device kernels' truncating rule on P rounded to bf16 (the
+ * reference's P is bf16; its bf16 exp and bf16 row-sum accumulation are
+ * not restated: l sums the bf16 P values in double).
  */
 #ifndef MX_ORACLE_H
 #define MX_ORACLE_H
@@ -78,7 +81,12 @@ typedef struct {
   float   softmax_scale;
   float   softcap;      /* 0 = off; else s <- cap*tanh(s/cap) after the scale      */
   int32_t v_fmt;        /* ORC_FMT_E4M3 / ORC_FMT_E3M2 (Q, K are always E4M3)      */
+  int32_t p_rule;       /* ORC_P_R1 (lib/golden requant) / ORC_P_R2 (device "target-0") */
 } orc_attn_params;
+
+#define ORC_P_R1 0
+#define ORC_P_R2 1
+#define ORC_MAX_BLOCK_N 4096
 
 /* Streaming MX attention over key blocks of block_n keys (block j covers keys
  * [j*block_n, (j+1)*block_n)).  split_len > 0 splits the keys into independent
@@ -115,6 +123,17 @@ uint8_t orc_r4_encode(float y);
 uint8_t orc_r4_quantize_block(const float *v, uint8_t *codes);
 void    orc_r4_quantize_rows(const float *x, int64_t rows, int64_t cols, uint8_t *codes, uint8_t *scales);
 int64_t orc_r4_check(uint32_t lo, uint32_t hi, int mode);
+
+/* Rule R2, the reference device kernels' P requant (kernels/flash_attention_mx_gqa/
+ * flash_mx_impl.hpp:53-77, 366-388, 485-501): bf16 P, block exponent se = unbiased
+ * exponent of the bf16 block maximum clamped to <= 0 (scale code se + 127), elements
+ * truncated to 3 mantissa bits, flushed below 2^(se-6), saturating at 448 * 2^se. */
+uint8_t orc_r2_encode(uint16_t bf16, int se);                 /* bf16_to_e4m3_scaled */
+int     orc_r2_scale_exp(float amax);                         /* se of an fp32 block max */
+uint8_t orc_r2_quantize_block(const float *p, int n, float *pb, uint8_t *codes);
+void    orc_r2_encode_array(const uint16_t *b, const int32_t *se, int64_t n, uint8_t *out);
+void    orc_r2_quantize_rows(const float *p, int64_t rows, int64_t cols, float *pb, uint8_t *codes,
+                             uint8_t *scales);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,8 @@ REF_DIR = os.path.join(HERE, "_ref")
 
 FMT_E4M3 = 0
 FMT_E3M2 = 1
+P_R1 = 0
+P_R2 = 1
 
 
 class AttnParams(ctypes.Structure):
@@ -25,6 +27,7 @@ class AttnParams(ctypes.Structure):
         ("seq_q", ctypes.c_int32), ("seq_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("causal", ctypes.c_int32), ("q_pos0", ctypes.c_int32), ("window", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("v_fmt", ctypes.c_int32),
+        ("p_rule", ctypes.c_int32),
     ]
 
 
@@ -69,6 +72,10 @@ def lib():
         L.orc_r4_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, u8p, u8p]
         L.orc_r4_check.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
         L.orc_r4_check.restype = ctypes.c_int64
+        L.orc_r2_encode.argtypes = [ctypes.c_uint16, ctypes.c_int]; L.orc_r2_encode.restype = ctypes.c_uint8
+        L.orc_r2_scale_exp.argtypes = [ctypes.c_float]; L.orc_r2_scale_exp.restype = ctypes.c_int
+        L.orc_r2_encode_array.argtypes = [P(ctypes.c_uint16), P(ctypes.c_int32), ctypes.c_int64, u8p]
+        L.orc_r2_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, f32p, u8p, u8p]
         _lib = L
     return _lib
 
@@ -139,9 +146,34 @@ def e4m3_encode(x):
     return out
 
 
-def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0, v_fmt=FMT_E4M3):
+def r2_encode(bf16, se):
+    """Rule R2 element codes of bf16 bit patterns (uint16) with block exponents se (int),
+    broadcast against each other."""
+    b, s = np.broadcast_arrays(np.asarray(bf16, np.uint16), np.asarray(se, np.int32))
+    b, s = np.ascontiguousarray(b), np.ascontiguousarray(s)
+    out = np.empty(b.shape, np.uint8)
+    lib().orc_r2_encode_array(b.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                              s.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), b.size, _u8(out))
+    return out
+
+
+def r2_quantize_rows(p):
+    """Rule R2 over 32-blocks along the last axis of fp32 P: returns (P rounded to bf16 as
+    float32, codes, scale codes)."""
+    p = np.ascontiguousarray(p, dtype=np.float32)
+    cols = p.shape[-1]
+    rows = p.size // cols
+    pb = np.empty(p.shape, np.float32)
+    codes = np.empty(p.shape, np.uint8)
+    scales = np.empty(tuple(p.shape[:-1]) + (cols // 32,), np.uint8)
+    lib().orc_r2_quantize_rows(_f32(p), rows, cols, _f32(pb), _u8(codes), _u8(scales))
+    return pb, codes, scales
+
+
+def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0, v_fmt=FMT_E4M3,
+                p_rule=P_R1):
     return AttnParams(B, Hq, Hkv, Sq, Sk, D, int(causal), q_pos0, window,
-                      float(scale if scale is not None else 1.0 / np.sqrt(D)), float(softcap), v_fmt)
+                      float(scale if scale is not None else 1.0 / np.sqrt(D)), float(softcap), v_fmt, p_rule)
 
 
 def attention(p, q, qs, k, ks, v, vs, block_n, split_len=0, heads=None, nthreads=None, out=None):

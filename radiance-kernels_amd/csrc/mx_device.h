@@ -201,13 +201,55 @@ __device__ __forceinline__ float p_bound(float p, const PTileBounds& b) {
   return __builtin_fminf(p < b.flush ? 0.0f : p, b.cap);
 }
 
-// Four P values (>= 0, finite) of one tile -> their R1 E4M3 codes (byte i = value i).
-__device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
+// Four already bounded values of one tile -> their E4M3 codes (byte i = value i).
+__device__ __forceinline__ uint32_t cvt_pack4(float y0, float y1, float y2, float y3, float scale) {
   v2s_t pk;
   pk = __builtin_nondeterministic_value(pk);        // both halves are written below
-  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, p_bound(p0, b), p_bound(p1, b), b.scale, false);
-  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, p_bound(p2, b), p_bound(p3, b), b.scale, true);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, y0, y1, scale, false);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, y2, y3, scale, true);
   return (uint32_t)(uint16_t)pk[0] | ((uint32_t)(uint16_t)pk[1] << 16);
+}
+
+// Four P values (>= 0, finite) of one tile -> their R1 E4M3 codes (byte i = value i).
+__device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
+  return cvt_pack4(p_bound(p0, b), p_bound(p1, b), p_bound(p2, b), p_bound(p3, b), b.scale);
+}
+
+// ---------------------------------------------------------------------------
+// Rule R2, the reference device kernels' P requant ("target-0", truncating;
+// kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:53-77, 366-388, 485-501), on P
+// rounded to bf16 (the reference's P is bf16).  Scale code sc = the bf16 exponent field
+// of the tile amax, clamped to <= 127 (se = sc - 127 <= 0).  Element: the bf16 P with
+// its mantissa cut to 3 bits, flushed when its exponent is below se - 6 (or its field
+// is 0).  P <= amax up to a rounding residue, so P / 2^se < 4 and the rule's saturation
+// never applies; the cut value divided by 2^se is then an E4M3 normal, which the
+// conversion encodes exactly.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {     // finite x >= 0: bf16 RNE, in the high half
+  const uint32_t b = __float_as_uint(x);
+  return (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+}
+
+__device__ __forceinline__ uint32_t r2_scale_code(float amax) {
+  const uint32_t f = bf16_rne_bits(amax) >> 23;
+  return f < 127u ? f : 127u;
+}
+
+struct PTileR2 {
+  float flush, scale;
+};
+
+__device__ __forceinline__ PTileR2 p_tile_r2(uint32_t sc) {
+  PTileR2 b;
+  b.flush = __uint_as_float(sc >= 6u ? (sc - 6u) << 23 : 0u);   // 2^(se - 6)
+  b.scale = __uint_as_float((sc << 23) | 0x400000u);             // 2^se (exponent field only)
+  return b;
+}
+
+// bf16 P (as float bits) -> the value R2 encodes, before the division by 2^se.
+__device__ __forceinline__ float r2_cut(uint32_t pb, const PTileR2& b) {
+  const float t = __uint_as_float(pb & 0xfff00000u);
+  return t < b.flush ? 0.0f : t;
 }
 
 }  // namespace mxfa

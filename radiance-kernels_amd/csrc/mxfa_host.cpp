@@ -43,6 +43,10 @@ const char* const kKernelNames[] = {
     "mxfa_decode_d64",         "mxfa_decode_d128",        "mxfa_decode_d256",     "mxfa_decode_d64_softcap",
     "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine", "mxfa_kv_append_e4m3",
     "mxfa_kv_append_e3m2",     "mxfa_kv_tail_update",     "mxfa_quant_rows_r4",
+    "mxfa_prefill_d64_r2",     "mxfa_prefill_d128_r2",    "mxfa_prefill_d256_r2",  "mxfa_prefill_d64_softcap_r2",
+    "mxfa_prefill_d128_softcap_r2", "mxfa_prefill_d256_softcap_r2", "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
+    "mxfa_decode_d256_r2",     "mxfa_decode_d64_softcap_r2", "mxfa_decode_d128_softcap_r2",
+    "mxfa_decode_d256_softcap_r2",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -128,6 +132,7 @@ mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
   if (!(p->softcap >= 0.0f) || !std::isfinite(p->softcap)) return fail(MXFA_ERR_INVALID_ARG, "softcap must be finite and >= 0");
   if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "v_fmt must be E4M3 or E3M2");
   if (p->block_n != 0 && p->block_n != 64) return fail(MXFA_ERR_UNSUPPORTED, "block_n must be 0 (default) or 64");
+  if (p->p_rule != MXFA_P_R1 && p->p_rule != MXFA_P_R2) return fail(MXFA_ERR_INVALID_ARG, "p_rule must be R1 or R2");
   if (decode) {
     if (p->seq_q != 1) return fail(MXFA_ERR_INVALID_ARG, "decode needs seq_q == 1");
     if (p->num_q_heads / p->num_kv_heads > 32)
@@ -164,9 +169,10 @@ FaArgs make_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* qs,
   return a;
 }
 
-const char* kernel_name(const char* kind, int D, bool softcap) {
+const char* kernel_name(const char* kind, const mxfa_attn_params* p) {
   static thread_local char buf[64];
-  std::snprintf(buf, sizeof buf, "mxfa_%s_d%d%s", kind, D, softcap ? "_softcap" : "");
+  std::snprintf(buf, sizeof buf, "mxfa_%s_d%d%s%s", kind, p->head_dim, p->softcap > 0.0f ? "_softcap" : "",
+                p->p_rule == MXFA_P_R2 ? "_r2" : "");
   return buf;
 }
 
@@ -319,8 +325,10 @@ mxfa_status mxfa_kv_append(const mxfa_kv_params* p, const float* k_new, const fl
 }
 
 mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, int64_t rows, int32_t cols,
-                                 float* p, uint8_t* codes, uint8_t* scales, float* row_sum, void* stream) {
+                                 int32_t p_rule, float* p, uint8_t* codes, uint8_t* scales, float* row_sum,
+                                 void* stream) {
   if (rows < 0 || cols <= 0 || cols % 32) return fail(MXFA_ERR_INVALID_ARG, "cols must be a positive multiple of 32");
+  if (p_rule != MXFA_P_R1 && p_rule != MXFA_P_R2) return fail(MXFA_ERR_INVALID_ARG, "p_rule must be R1 or R2");
   if (!(c > 0.0f) || !std::isfinite(c)) return fail(MXFA_ERR_INVALID_ARG, "c must be finite and > 0");
   if (rows == 0) return MXFA_OK;
   if (!s || !row_max || !p || !codes || !scales || !row_sum) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
@@ -330,7 +338,8 @@ mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, 
   if (mxfa_status st = module_for_current(&dm)) return st;
   dim3 grid((unsigned)((rows + 255) / 256));
   int cols_i = cols;
-  void* args[] = {(void*)&s, (void*)&row_max, &c, &rows, &cols_i, &p, &codes, &scales, &row_sum};
+  int rule = p_rule;
+  void* args[] = {(void*)&s, (void*)&row_max, &c, &rows, &cols_i, &p, &codes, &scales, &row_sum, &rule};
   return launch(dm, "mxfa_softmax_requant_rows", grid, dim3(256), args, stream);
 }
 
@@ -358,7 +367,7 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   a.n_qblk = (p->seq_q + a.qpw - 1) / a.qpw;
   dim3 grid((unsigned)a.n_qblk, (unsigned)(p->batch * p->num_kv_heads * (a.group / a.hpw)));
   void* args[] = {&a};
-  return launch(dm, kernel_name("prefill", p->head_dim, p->softcap > 0.0f), grid, dim3(256), args, stream);
+  return launch(dm, kernel_name("prefill", p), grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* split_len, size_t* workspace_bytes) {
@@ -396,7 +405,7 @@ mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8
   const int nw = p->head_dim == 256 ? 2 : 4;   // waves per decode workgroup (LDS-limited at D = 256)
   dim3 grid((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads));
   void* args[] = {&a};
-  if (mxfa_status st = launch(dm, kernel_name("decode", p->head_dim, p->softcap > 0.0f), grid, dim3(64 * nw), args, stream))
+  if (mxfa_status st = launch(dm, kernel_name("decode", p), grid, dim3(64 * nw), args, stream))
     return st;
   return launch(dm, "mxfa_decode_combine", dim3((unsigned)nbh), dim3((unsigned)p->head_dim), args, stream);
 }

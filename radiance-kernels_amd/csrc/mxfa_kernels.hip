@@ -490,11 +490,49 @@ __device__ __forceinline__ void p_tile16(const v16f& s, float c, float mcn, uint
   for (int g = 0; g < 4; g++) w[g] = p_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], bnd);
 }
 
+// The same step with rule R2: P rounded to bf16 (the P written and summed), the scale
+// from the bf16 tile amax, codes by mantissa truncation.
+__device__ __forceinline__ uint32_t p_tile_scale_r2(float bmax, float mu, float c) {
+  return r2_scale_code(__builtin_amdgcn_exp2f((bmax - mu) * c));
+}
+
+__device__ __forceinline__ void p_tile16_r2(const v16f& s, float c, float mcn, uint32_t sc, float (&p)[16],
+                                            uint32_t (&w)[4], float& lsum) {
+  const PTileR2 bnd = p_tile_r2(sc);
+  float y[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const uint32_t pb = bf16_rne_bits(__builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c, mcn)));
+    p[i] = __uint_as_float(pb);
+    lsum += p[i];
+    y[i] = r2_cut(pb, bnd);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; g++) w[g] = cvt_pack4(y[4 * g], y[4 * g + 1], y[4 * g + 2], y[4 * g + 3], bnd.scale);
+}
+
+// P rules of the attention kernels (template argument PR).
+enum { P_R1 = 0, P_R2 = 1 };
+
+template <int PR>
+__device__ __forceinline__ uint32_t p_scale(float bmax, float mu, float c) {
+  return PR == P_R2 ? p_tile_scale_r2(bmax, mu, c) : p_tile_scale(bmax, mu, c);
+}
+
+template <int PR>
+__device__ __forceinline__ void p_tile(const v16f& s, float c, float mcn, uint32_t sc, float (&p)[16],
+                                       uint32_t (&w)[4], float& lsum) {
+  if constexpr (PR == P_R2)
+    p_tile16_r2(s, c, mcn, sc, p, w, lsum);
+  else
+    p_tile16(s, c, mcn, sc, p, w, lsum);
+}
+
 // Test entry: the routine above on caller scores, one thread per row, 32-blocks along
 // the row.  Outputs P, codes, scales, and the row sums of P.
-extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
-    const float* s, const float* row_max, float c, int64_t rows, int cols, float* p, uint8_t* codes,
-    uint8_t* scales, float* row_sum) {
+template <int PR>
+__device__ void softmax_requant_rows(const float* s, const float* row_max, float c, int64_t rows, int cols, float* p,
+                                     uint8_t* codes, uint8_t* scales, float* row_sum) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   const float mu = row_max[r], mcn = -(mu * c);
@@ -512,11 +550,11 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
     float bmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; i++) bmax = fmaxf(bmax, fmaxf(a[i], b[i]));
-    const uint32_t sc = p_tile_scale(bmax, mu, c);
+    const uint32_t sc = p_scale<PR>(bmax, mu, c);
     float pa[16], pb[16];
     uint32_t wa[4], wb[4];
-    p_tile16(a, c, mcn, sc, pa, wa, lsum);
-    p_tile16(b, c, mcn, sc, pb, wb, lsum);
+    p_tile<PR>(a, c, mcn, sc, pa, wa, lsum);
+    p_tile<PR>(b, c, mcn, sc, pb, wb, lsum);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       p[off + i] = pa[i];
@@ -530,6 +568,15 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
     scales[r * (cols / 32) + j] = (uint8_t)sc;
   }
   row_sum[r] = lsum;
+}
+
+extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
+    const float* s, const float* row_max, float c, int64_t rows, int cols, float* p, uint8_t* codes,
+    uint8_t* scales, float* row_sum, int p_rule) {
+  if (p_rule == P_R2)
+    softmax_requant_rows<P_R2>(s, row_max, c, rows, cols, p, codes, scales, row_sum);
+  else
+    softmax_requant_rows<P_R1>(s, row_max, c, rows, cols, p, codes, scales, row_sum);
 }
 
 // mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
@@ -551,7 +598,7 @@ __device__ __forceinline__ void qk_tiles(v16f (&s)[BN / 32], const v4i* qb, cons
 
 // Softmax, P requant and O^T += V^T P^T for one key block whose scores are in s.
 // mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
-template <int D, bool SOFTCAP>
+template <int D, bool SOFTCAP, int PR>
 __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32], const uint8_t* sV,
                                            const uint8_t* sVs, int key0, int klo, int khi, bool mask,
                                            const FaArgs& a, int lane) {
@@ -610,18 +657,18 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32],
   float corr = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((st.m - mu) * c);
   st.m = m_new;
 
-  // ---- P tiles: scale from the exact tile amax, R1 codes
+  // ---- P tiles: scale from the exact tile amax, R1 (or R2) codes
   const float mcn = -(mu * c);
   float lsum = 0.0f;
   v8i pb[NT / 2];                    // P codes: B operand of each 64-key PV step
   int psc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
-    const uint32_t sc = p_tile_scale(bmax[t], mu, c);
+    const uint32_t sc = p_scale<PR>(bmax[t], mu, c);
     psc[t] = (int)sc;
     float p[16];
     uint32_t w[4];
-    p_tile16(s[t], c, mcn, sc, p, w, lsum);
+    p_tile<PR>(s[t], c, mcn, sc, p, w, lsum);
 #pragma unroll
     for (int g = 0; g < 4; g++) pb[t >> 1][4 * (t & 1) + g] = (int)w[g];
   }
@@ -660,13 +707,13 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32],
 }
 
 // One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
-template <int D, bool SOFTCAP>
+template <int D, bool SOFTCAP, int PR>
 __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
                                            const uint8_t* sVs, int key0, int klo, int khi, bool mask,
                                            const FaArgs& a, int lane) {
   v16f s[BN / 32];
   qk_tiles<D>(s, qb, sKb, lane);
-  softmax_pv<D, SOFTCAP>(st, s, sV, sVs, key0, klo, khi, mask, a, lane);
+  softmax_pv<D, SOFTCAP, PR>(st, s, sV, sVs, key0, klo, khi, mask, a, lane);
 }
 
 // Q operand (B of S^T = K Q^T, bf16) for query row `qrow` (zeros if invalid): MFMA kk
@@ -707,7 +754,7 @@ __device__ __forceinline__ void load_q_split(v4i* qb, const uint8_t* qrow, const
 // The workgroup covers hpw heads of one KV group x qpw positions, so the K/V
 // tile in LDS serves 4 x 32 query rows.  grid = (n_qblk, B * Hkv * group / hpw).
 // ---------------------------------------------------------------------------
-template <int D, bool SOFTCAP>
+template <int D, bool SOFTCAP, int PR>
 __device__ void prefill_impl(const FaArgs& a) {
   __shared__ __attribute__((aligned(16))) uint8_t sK[2][Lds<D>::TILEK];
   __shared__ __attribute__((aligned(16))) uint8_t sV[2][Lds<D>::TILE];
@@ -771,7 +818,7 @@ __device__ void prefill_impl(const FaArgs& a) {
       const bool need_mask = __builtin_amdgcn_readfirstlane(
           (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
           (qw0 + 31 >= a.Sq));
-      wave_block<D, SOFTCAP>(st, qb, sK[buf], sV[buf], sVs[buf], key0, klo, khi, need_mask, a, lane);
+      wave_block<D, SOFTCAP, PR>(st, qb, sK[buf], sV[buf], sVs[buf], key0, klo, khi, need_mask, a, lane);
     }
   };
   if constexpr (D <= 128) {
@@ -826,14 +873,20 @@ __device__ void prefill_impl(const FaArgs& a) {
   }
 }
 
-#define MXFA_PREFILL(D, SC, NAME)                                                      \
-  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { prefill_impl<D, SC>(a); }
-MXFA_PREFILL(64, false, mxfa_prefill_d64)
-MXFA_PREFILL(128, false, mxfa_prefill_d128)
-MXFA_PREFILL(256, false, mxfa_prefill_d256)
-MXFA_PREFILL(64, true, mxfa_prefill_d64_softcap)
-MXFA_PREFILL(128, true, mxfa_prefill_d128_softcap)
-MXFA_PREFILL(256, true, mxfa_prefill_d256_softcap)
+#define MXFA_PREFILL(D, SC, PR, NAME)                                                  \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { prefill_impl<D, SC, PR>(a); }
+MXFA_PREFILL(64, false, P_R1, mxfa_prefill_d64)
+MXFA_PREFILL(128, false, P_R1, mxfa_prefill_d128)
+MXFA_PREFILL(256, false, P_R1, mxfa_prefill_d256)
+MXFA_PREFILL(64, true, P_R1, mxfa_prefill_d64_softcap)
+MXFA_PREFILL(128, true, P_R1, mxfa_prefill_d128_softcap)
+MXFA_PREFILL(256, true, P_R1, mxfa_prefill_d256_softcap)
+MXFA_PREFILL(64, false, P_R2, mxfa_prefill_d64_r2)
+MXFA_PREFILL(128, false, P_R2, mxfa_prefill_d128_r2)
+MXFA_PREFILL(256, false, P_R2, mxfa_prefill_d256_r2)
+MXFA_PREFILL(64, true, P_R2, mxfa_prefill_d64_softcap_r2)
+MXFA_PREFILL(128, true, P_R2, mxfa_prefill_d128_softcap_r2)
+MXFA_PREFILL(256, true, P_R2, mxfa_prefill_d256_softcap_r2)
 
 // ---------------------------------------------------------------------------
 // Decode (q_len = 1, split-KV).  The keys of each (b, KV head) are cut into
@@ -851,7 +904,7 @@ MXFA_PREFILL(256, true, mxfa_prefill_d256_softcap)
 // per-wave LDS and register footprints give two workgroups per CU, whose waves hide
 // each other's load latency.
 // ---------------------------------------------------------------------------
-template <int D, bool SOFTCAP>
+template <int D, bool SOFTCAP, int PR>
 __device__ void decode_split_impl(const FaArgs& a) {
   constexpr int NW = 4;
   constexpr int NT = BN / 32;
@@ -943,7 +996,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
     }
     // LDS operations of one wave complete in order: the V tile written above is in place
     // for the transposed reads, and the next block's writes follow this block's reads
-    softmax_pv<D, SOFTCAP>(st, sc, sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
+    softmax_pv<D, SOFTCAP, PR>(st, sc, sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
   }
 
   // partial outputs (unnormalized O, m in x units, full l)
@@ -967,7 +1020,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
 // Waves per decode workgroup (each wave has private LDS tiles).
 template <int D> struct DecodeWaves { static constexpr int N = D == 256 ? 2 : 4; };
 
-template <int D, bool SOFTCAP>
+template <int D, bool SOFTCAP, int PR>
 __device__ void decode_impl(const FaArgs& a) {
   constexpr int NW = DecodeWaves<D>::N;
   __shared__ __attribute__((aligned(16))) uint8_t sK[NW][Lds<D>::TILEK];
@@ -1043,7 +1096,7 @@ __device__ void decode_impl(const FaArgs& a) {
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     // columns >= group are padding and must be masked
-    wave_block<D, SOFTCAP>(st, qb, sK[wave], sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
+    wave_block<D, SOFTCAP, PR>(st, qb, sK[wave], sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
     __builtin_amdgcn_wave_barrier();
   }
 
@@ -1065,16 +1118,22 @@ __device__ void decode_impl(const FaArgs& a) {
   }
 }
 
-#define MXFA_DECODE_SPLIT(D, SC, NAME)                                                 \
-  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC>(a); }
-#define MXFA_DECODE(D, SC, NAME)                                                       \
-  extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<D>::N) NAME(FaArgs a) { decode_impl<D, SC>(a); }
-MXFA_DECODE_SPLIT(64, false, mxfa_decode_d64)
-MXFA_DECODE_SPLIT(128, false, mxfa_decode_d128)
-MXFA_DECODE(256, false, mxfa_decode_d256)
-MXFA_DECODE_SPLIT(64, true, mxfa_decode_d64_softcap)
-MXFA_DECODE_SPLIT(128, true, mxfa_decode_d128_softcap)
-MXFA_DECODE(256, true, mxfa_decode_d256_softcap)
+#define MXFA_DECODE_SPLIT(D, SC, PR, NAME)                                             \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC, PR>(a); }
+#define MXFA_DECODE(D, SC, PR, NAME)                                                   \
+  extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<D>::N) NAME(FaArgs a) { decode_impl<D, SC, PR>(a); }
+MXFA_DECODE_SPLIT(64, false, P_R1, mxfa_decode_d64)
+MXFA_DECODE_SPLIT(128, false, P_R1, mxfa_decode_d128)
+MXFA_DECODE(256, false, P_R1, mxfa_decode_d256)
+MXFA_DECODE_SPLIT(64, true, P_R1, mxfa_decode_d64_softcap)
+MXFA_DECODE_SPLIT(128, true, P_R1, mxfa_decode_d128_softcap)
+MXFA_DECODE(256, true, P_R1, mxfa_decode_d256_softcap)
+MXFA_DECODE_SPLIT(64, false, P_R2, mxfa_decode_d64_r2)
+MXFA_DECODE_SPLIT(128, false, P_R2, mxfa_decode_d128_r2)
+MXFA_DECODE(256, false, P_R2, mxfa_decode_d256_r2)
+MXFA_DECODE_SPLIT(64, true, P_R2, mxfa_decode_d64_softcap_r2)
+MXFA_DECODE_SPLIT(128, true, P_R2, mxfa_decode_d128_softcap_r2)
+MXFA_DECODE(256, true, P_R2, mxfa_decode_d256_softcap_r2)
 
 // Merge nparts partials per (b, query head) in part order: O = sum_i O_i 2^{(m_i - M) c} / sum_i l_i 2^{(m_i - M) c}.
 // One workgroup of D threads per query head.

@@ -28,6 +28,8 @@ LIB_PATH = os.path.join(HERE, "libmxfa.so")
 
 FMT_E4M3 = 0
 FMT_E3M2 = 1
+P_R1 = 0        # P requant rule of lib/golden (default)
+P_R2 = 1        # the reference device kernels' truncating "target-0" rule
 DEFAULT_BLOCK_N = 64
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "HIP error", 4: "code object error",
@@ -46,15 +48,15 @@ class AttnParams(ctypes.Structure):
         ("seq_q", ctypes.c_int32), ("seq_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("causal", ctypes.c_int32), ("q_pos0", ctypes.c_int32), ("window", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("v_fmt", ctypes.c_int32),
-        ("block_n", ctypes.c_int32),
+        ("block_n", ctypes.c_int32), ("p_rule", ctypes.c_int32),
     ]
 
 
 def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0,
-                v_fmt=FMT_E4M3, block_n=0):
+                v_fmt=FMT_E4M3, block_n=0, p_rule=P_R1):
     return AttnParams(B, Hq, Hkv, Sq, Sk, D, int(bool(causal)), int(q_pos0), int(window),
                       float(scale if scale is not None else 1.0 / math.sqrt(D)), float(softcap), int(v_fmt),
-                      int(block_n))
+                      int(block_n), int(p_rule))
 
 
 class KvParams(ctypes.Structure):
@@ -84,8 +86,8 @@ def lib():
         L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
         L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
         L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
-        L.mxfa_softmax_requant.argtypes = [f32p, f32p, ctypes.c_float, ctypes.c_int64, ctypes.c_int32, f32p,
-                                           u8p, u8p, f32p, vp]
+        L.mxfa_softmax_requant.argtypes = [f32p, f32p, ctypes.c_float, ctypes.c_int64, ctypes.c_int32,
+                                           ctypes.c_int32, f32p, u8p, u8p, f32p, vp]
         L.mxfa_fill_normal.argtypes = [f32p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp]
         L.mxfa_kv_append.argtypes = [P(KvParams), f32p, f32p, ctypes.c_int32, ctypes.c_int32] + [u8p] * 4 + [f32p, vp]
         L.mxfa_status_string.argtypes = [ctypes.c_int]
@@ -156,9 +158,9 @@ def quantize_cols(x, fmt=FMT_E4M3, stream=None):
     return codes, scales
 
 
-def softmax_requant(s, row_max, c, stream=None):
+def softmax_requant(s, row_max, c, p_rule=P_R1, stream=None):
     """The kernels' softmax-requant step on scores s [..., cols] (cols % 32 == 0) with
-    per-row maxima row_max [...]: returns (p, codes, scales, row_sum)
+    per-row maxima row_max [...] under P rule p_rule: returns (p, codes, scales, row_sum)
     (mxfa_softmax_requant)."""
     import torch
     assert s.is_cuda and s.dtype == torch.float32 and s.is_contiguous()
@@ -170,8 +172,8 @@ def softmax_requant(s, row_max, c, stream=None):
     codes = torch.empty(s.shape, dtype=torch.uint8, device=s.device)
     scales = torch.empty(tuple(s.shape[:-1]) + (cols // 32,), dtype=torch.uint8, device=s.device)
     row_sum = torch.empty(tuple(s.shape[:-1]), dtype=torch.float32, device=s.device)
-    _check(lib().mxfa_softmax_requant(_ptr(s), _ptr(row_max), float(c), rows, cols, _ptr(p), _ptr(codes),
-                                      _ptr(scales), _ptr(row_sum), _stream(stream)))
+    _check(lib().mxfa_softmax_requant(_ptr(s), _ptr(row_max), float(c), rows, cols, int(p_rule), _ptr(p),
+                                      _ptr(codes), _ptr(scales), _ptr(row_sum), _stream(stream)))
     return p, codes, scales, row_sum
 
 

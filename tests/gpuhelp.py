@@ -35,7 +35,7 @@ def gen_qkv(B, Hq, Hkv, Sq, Sk, D, seed, outlier_p=0.0, q_mul=1.0, v_fmt=mxfa.FM
 def oracle_params(p):
     return O.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim,
                          causal=bool(p.causal), q_pos0=p.q_pos0, window=p.window, scale=p.softmax_scale,
-                         softcap=p.softcap, v_fmt=p.v_fmt)
+                         softcap=p.softcap, v_fmt=p.v_fmt, p_rule=p.p_rule)
 
 
 def errors(got, want):

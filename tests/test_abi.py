@@ -31,7 +31,8 @@ def test_code_object_present_and_for_gfx950():
     data = open(path, "rb").read()
     assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     assert b"gfx950" in data
-    for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows"):
+    for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows",
+              "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2"):
         assert k.encode() in data
 
 
@@ -58,12 +59,14 @@ def _call_prefill(p):
     (dict(window=-1), 1),
     (dict(softcap=-1.0), 1),
     (dict(block_n=128), 2),
+    (dict(p_rule=2), 1),
+    (dict(p_rule=-1), 1),
 ])
 def test_prefill_argument_validation(kw, status):
-    a = dict(B=1, Hq=2, Hkv=2, Sq=32, Sk=64, D=64, window=0, softcap=0.0, block_n=0)
+    a = dict(B=1, Hq=2, Hkv=2, Sq=32, Sk=64, D=64, window=0, softcap=0.0, block_n=0, p_rule=0)
     a.update(kw)
     p = mxfa.make_params(a["B"], a["Hq"], a["Hkv"], a["Sq"], a["Sk"], a["D"], window=a["window"],
-                         softcap=a["softcap"], block_n=a["block_n"])
+                         softcap=a["softcap"], block_n=a["block_n"], p_rule=a["p_rule"])
     assert _call_prefill(p) == status
     assert mxfa.lib().mxfa_last_error()
 
@@ -97,9 +100,10 @@ def test_quantize_argument_validation():
     assert L.mxfa_quantize_rows(None, 0, 64, 0, None, None, None) == 0     # empty input: no-op
     assert L.mxfa_quantize_cols(None, 1, 48, 64, 0, None, None, None) == 1
     assert L.mxfa_quantize_cols(None, 0, 64, 64, 0, None, None, None) == 0
-    assert L.mxfa_softmax_requant(None, None, 1.0, 4, 33, None, None, None, None, None) == 1
-    assert L.mxfa_softmax_requant(None, None, 0.0, 4, 32, None, None, None, None, None) == 1
-    assert L.mxfa_softmax_requant(None, None, 1.0, 0, 32, None, None, None, None, None) == 0
+    assert L.mxfa_softmax_requant(None, None, 1.0, 4, 33, 0, None, None, None, None, None) == 1
+    assert L.mxfa_softmax_requant(None, None, 0.0, 4, 32, 0, None, None, None, None, None) == 1
+    assert L.mxfa_softmax_requant(None, None, 1.0, 4, 32, 3, None, None, None, None, None) == 1   # bad rule
+    assert L.mxfa_softmax_requant(None, None, 1.0, 0, 32, 1, None, None, None, None, None) == 0
 
 
 def test_kv_append_argument_validation():

@@ -15,9 +15,9 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.0, v_fmt=mxfa.FMT_E4M3,
-             seed=0, outlier_p=0.0, q_mul=1.0, heads=None, check_codes=True):
+             seed=0, outlier_p=0.0, q_mul=1.0, heads=None, check_codes=True, p_rule=mxfa.P_R1):
     print(f"case B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Sk{Sk} D{D} causal{causal} q_pos0 {q_pos0} window {window} "
-          f"softcap {softcap} v_fmt {v_fmt} seed {seed}", flush=True)
+          f"softcap {softcap} v_fmt {v_fmt} seed {seed} p_rule {p_rule}", flush=True)
     fp, dev, host = gen_qkv(B, Hq, Hkv, Sq, Sk, D, seed, outlier_p=outlier_p, q_mul=q_mul, v_fmt=v_fmt)
     if check_codes:
         oq, oqs = O.quantize_rows(np_(fp["Q"]), O.FMT_E4M3)
@@ -27,7 +27,7 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
         np.testing.assert_array_equal(host["v"], ov)
         np.testing.assert_array_equal(host["vs"], ovs)
     p = mxfa.make_params(B, Hq, Hkv, Sq, Sk, D, causal=causal, q_pos0=q_pos0, window=window, softcap=softcap,
-                         v_fmt=v_fmt)
+                         v_fmt=v_fmt, p_rule=p_rule)
     out = torch.full((B, Hq, Sq, D), float("nan"), dtype=torch.float32, device=DEV)
     mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
     torch.cuda.synchronize()
@@ -108,10 +108,11 @@ def test_baseline_configs_sampled_heads(cfg):
                  heads=[3], check_codes=False)
 
 
-def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=0.0):
-    print(f"decode B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} seed {seed}", flush=True)
+def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=0.0, p_rule=mxfa.P_R1):
+    print(f"decode B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} seed {seed} p_rule {p_rule}", flush=True)
     fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L, D, seed, v_fmt=v_fmt)
-    p = mxfa.make_params(B, Hq, Hkv, 1, L, D, causal=True, q_pos0=L - 1, softcap=softcap, v_fmt=v_fmt)
+    p = mxfa.make_params(B, Hq, Hkv, 1, L, D, causal=True, q_pos0=L - 1, softcap=softcap, v_fmt=v_fmt,
+                         p_rule=p_rule)
     split_len, _ = mxfa.decode_plan(p)
     out = torch.full((B, Hq, 1, D), float("nan"), dtype=torch.float32, device=DEV)
     mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
@@ -145,3 +146,59 @@ def test_decode_config5_sampled():
     out2 = mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
+
+
+# ---- P rule R2: the reference device kernels' truncating "target-0" requant of bf16 P
+# (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:53-77, 366-388), same tolerance
+# against the oracle run with the same rule.
+
+def test_r2_reference_gqa_tile():
+    p, dev, out = run_case(1, 8, 2, 64, 256, 64, causal=True, q_pos0=64, seed=2, p_rule=mxfa.P_R2)
+    p1 = mxfa.make_params(1, 8, 2, 64, 256, 64, causal=True, q_pos0=64)
+    out1 = mxfa.prefill(p1, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
+    torch.cuda.synchronize()
+    assert not torch.equal(out, out1)                 # the rule is in effect
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_r2_causal_gqa_head_dims(D):
+    run_case(2, 8, 2, 160, 160, D, causal=True, seed=40 + D, p_rule=mxfa.P_R2)
+
+
+def test_r2_ragged_softcap_window_e3m2():
+    run_case(2, 4, 1, 45, 224, 128, causal=True, q_pos0=179, seed=41, p_rule=mxfa.P_R2)
+    run_case(1, 4, 2, 384, 384, 256, causal=True, window=128, softcap=50.0, v_fmt=mxfa.FMT_E3M2, seed=42,
+             p_rule=mxfa.P_R2)
+    run_case(1, 8, 2, 256, 256, 128, causal=True, outlier_p=0.01, seed=43, p_rule=mxfa.P_R2)
+
+
+def test_r2_config3_sampled_heads():
+    run_case(2, 32, 8, 4096, 4096, 128, causal=True, outlier_p=0.01, seed=44, heads=[7, 40], check_codes=False,
+             p_rule=mxfa.P_R2)
+
+
+def test_r2_decode():
+    run_decode(4, 32, 8, 1024, 128, seed=45, p_rule=mxfa.P_R2)
+    run_decode(3, 8, 2, 480, 64, seed=46, v_fmt=mxfa.FMT_E3M2, p_rule=mxfa.P_R2)
+    run_decode(2, 16, 8, 2080, 256, seed=47, softcap=30.0, p_rule=mxfa.P_R2)
+
+
+def test_reference_format_operands():
+    """Operands exported to the reference's fa_data.h layout (header text) and imported
+    back give the same prefill output bit for bit (the omitted key blocks are causally
+    masked), under both P rules."""
+    import fa_data as F
+    Hq, Hkv, Sq, Sk, D, q_pos0 = 8, 2, 64, 256, 64, 64
+    fp, dev, host = gen_qkv(1, Hq, Hkv, Sq, Sk, D, 50)
+    names = ("q", "qs", "k", "ks", "v", "vs")
+    fd = F.read_header(F.header_text(F.export_fa_data(*(host[n] for n in names), block_n=64, q_pos0=q_pos0)))
+    imp, prm = F.import_fa_data(fd)
+    assert prm["block_n"] == mxfa.DEFAULT_BLOCK_N
+    idev = [torch.from_numpy(a).to(DEV) for a in imp]
+    for rule in (mxfa.P_R1, mxfa.P_R2):
+        p = mxfa.make_params(1, prm["Hq"], prm["Hkv"], prm["Sq"], prm["Sk"], prm["D"], causal=prm["causal"],
+                             q_pos0=prm["q_pos0"], scale=prm["scale"], p_rule=rule)
+        want = mxfa.prefill(p, *(dev[n] for n in names))
+        got = mxfa.prefill(p, *idev)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)

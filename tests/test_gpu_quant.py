@@ -145,6 +145,52 @@ def test_softmax_requant_bit_exact(c):
     np.testing.assert_allclose(rsum, p.astype(np.float64).sum(axis=1), rtol=1e-5, atol=1e-30)
 
 
+@pytest.mark.parametrize("c", [0.08838834764831845 * LOG2E, 1.0])
+def test_softmax_requant_r2_bit_exact(c):
+    """Rule R2 on the device: P is bf16 (low half zero), the codes are exactly the oracle's
+    R2 codes of that P with se = sc - 127, sc is the bf16 exponent field of the tile amax
+    (127 in the row-max tile), the largest code of each nonzero tile decodes into [1, 2),
+    and the row sums add the bf16 P."""
+    rng = np.random.default_rng(302)
+    rows, cols = 8192, 128
+    s, rmax = softmax_inputs(rng, rows, cols, c)
+    p, codes, scales, rsum = mxfa.softmax_requant(torch.from_numpy(s).to(DEV), torch.from_numpy(rmax).to(DEV), c,
+                                                  p_rule=mxfa.P_R2)
+    p, codes, scales, rsum = (np_(t) for t in (p, codes, scales, rsum))
+    nb = cols // 32
+    pbits = p.view(np.uint32)
+    assert np.all((pbits & 0xFFFF) == 0)
+    se = np.repeat(scales.astype(np.int32), 32, axis=1) - 127
+    want = O.r2_encode((pbits >> 16).astype(np.uint16), se)
+    bad = np.argwhere(codes != want)
+    assert len(bad) == 0, [(float(p[i, j]), int(se[i, j]), int(codes[i, j]), int(want[i, j])) for i, j in bad[:8]]
+    # scale: bf16 exponent field of amax = 2^((max s - m) c); accept either neighbour of a
+    # bf16 rounding boundary (host and device exp2 may differ by an ulp)
+    bmax = s.reshape(rows, nb, 32).max(axis=2).astype(np.float64)
+    arg = (bmax - rmax[:, None].astype(np.float64)) * c
+    amax = np.exp2(arg)
+    L = O.lib()
+
+    def field(a):
+        return min(127, L.orc_f32_to_bf16(float(np.float32(a))) >> 7)
+
+    lo = np.array([[field(a * (1 - 2.0 ** -21)) for a in r] for r in amax])
+    hi = np.array([[field(a * (1 + 2.0 ** -21)) for a in r] for r in amax])
+    ok = (scales == lo) | (scales == hi)
+    assert ok.all(), np.argwhere(~ok)[:8]
+    assert np.all(scales[arg == 0.0] == 127)
+    dec = np.array([L.orc_e4m3_decode(cc) for cc in range(256)], np.float64)[codes]
+    tmax = dec.reshape(rows, nb, 32).max(axis=2)
+    nz = p.reshape(rows, nb, 32).max(axis=2) > 0
+    assert np.all((tmax[nz] >= 1.0) & (tmax[nz] < 4.0)) and np.mean(tmax[nz] < 2.0) > 0.999
+    assert (codes == 0).any() and (scales < 100).any()
+    # P and sums: bf16 rounding of the exponential, summed in fp32
+    Pref = np.exp2((s.astype(np.float64) - rmax[:, None]) * c)
+    big = Pref > 2.0 ** -100
+    assert (np.abs(p[big] - Pref[big]) / Pref[big]).max() < 2.0 ** -8 + 1e-4
+    np.testing.assert_allclose(rsum, p.astype(np.float64).sum(axis=1), rtol=1e-5, atol=1e-30)
+
+
 def L_scale(a):
     return O.lib().orc_scale_code(float(a), O.FMT_E4M3)
 

@@ -8,9 +8,10 @@ import oracle as O
 from mxdata import dequant_cols, dequant_rows, normal_inputs, quantize_qkv, rel_l2
 
 
-def _single_block_closed_form(q, qs, k, ks, v, vs, scale, mask=None, softcap=0.0):
+def _single_block_closed_form(q, qs, k, ks, v, vs, scale, mask=None, softcap=0.0, p_rule=O.P_R1):
     """One key block: O = sum_k Pq_k V_k / sum_k P_k with P = fp32(exp(S - max S)) and
-    Pq the R1 requant of P per 32 keys (quantizer pinned separately)."""
+    Pq the R1 requant of P per 32 keys (quantizer pinned separately); with rule R2, P is
+    first rounded to bf16 and requantized by R2 (pinned separately)."""
     Qd = dequant_rows(q, qs, O.FMT_E4M3)
     Kd = dequant_rows(k, ks, O.FMT_E4M3)
     Vd = dequant_cols(v, vs, O.FMT_E4M3)
@@ -21,6 +22,10 @@ def _single_block_closed_form(q, qs, k, ks, v, vs, scale, mask=None, softcap=0.0
         S = np.where(mask, -np.inf, S)
     m = S.max(axis=1, keepdims=True)
     P = np.where(np.isinf(S), 0.0, np.exp(S - m)).astype(np.float32)
+    if p_rule == O.P_R2:
+        P, pc, ps = O.r2_quantize_rows(P)
+        Pq = dequant_rows(pc, ps, O.FMT_E4M3)
+        return (Pq @ Vd) / P.astype(np.float64).sum(axis=1, keepdims=True)
     pc, ps = O.quantize_rows(P, O.FMT_E4M3)
     Pq = dequant_rows(pc, ps, O.FMT_E4M3)
     return (Pq @ Vd) / P.astype(np.float64).sum(axis=1, keepdims=True)
@@ -36,6 +41,27 @@ def test_single_block_closed_form(causal):
     mask = np.triu(np.ones((S, S), bool), 1) if causal else None
     want = _single_block_closed_form(q[0, 0], qs[0, 0], k[0, 0], ks[0, 0], v[0, 0], vs[0, 0], p.softmax_scale, mask)
     np.testing.assert_allclose(o[0, 0], want, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_single_block_closed_form_r2(causal):
+    """Rule R2 (the reference device kernels' truncating requant of bf16 P) in the
+    recurrence: P rounded to bf16 for both the PV codes and the row sum."""
+    B, H, S, D = 1, 1, 96, 64
+    Q, K, V = normal_inputs(B, H, H, S, S, D, seed=13)
+    q, qs, k, ks, v, vs = quantize_qkv(Q, K, V)
+    p = O.make_params(B, H, H, S, S, D, causal=causal, p_rule=O.P_R2)
+    o = O.attention(p, q, qs, k, ks, v, vs, block_n=128)
+    mask = np.triu(np.ones((S, S), bool), 1) if causal else None
+    want = _single_block_closed_form(q[0, 0], qs[0, 0], k[0, 0], ks[0, 0], v[0, 0], vs[0, 0], p.softmax_scale, mask,
+                                     p_rule=O.P_R2)
+    np.testing.assert_allclose(o[0, 0], want, rtol=1e-6, atol=1e-7)
+    # truncation only lowers P codes: R2 differs from R1 by at most the 2^-3 relative
+    # truncation step of each P, and it is not the R1 result
+    o1 = O.attention(O.make_params(B, H, H, S, S, D, causal=causal), q, qs, k, ks, v, vs, block_n=128)
+    dense = O.attention_dense(O.make_params(B, H, H, S, S, D, causal=causal), q, qs, k, ks, v, vs)
+    assert not np.array_equal(o, o1)
+    assert rel_l2(o, dense) < 0.15 and rel_l2(o1, dense) < rel_l2(o, dense)
 
 
 def test_blocking_exact_when_max_in_first_key():

@@ -232,3 +232,87 @@ def test_r4_scale_is_ceil_log2_amax_over_448():
         assert s == min(max(e + 127, 0), 254), (a, s, e)
     _, sc0 = O.r4_quantize_rows(np.zeros((1, 32), np.float32))
     assert sc0[0, 0] == 0
+
+
+# ---- rule R2: the reference device kernels' truncating P requant
+# (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:53-77)
+
+def _all_bf16_finite():
+    b = np.arange(0, 0x10000, dtype=np.uint32)
+    b = b[((b >> 7) & 0xFF) != 0xFF]                      # finite patterns of both signs
+    return b.astype(np.uint16), (b << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("se", [0, -1, -3, -6, -7, -40, -119, -120, -121, -126, -127])
+def test_r2_element_rule_is_truncation_on_the_e4m3_grid(se):
+    """Every finite bf16 with block exponent se: the code's value is |v| * 2^-se with its
+    binary mantissa cut to 3 bits (floor), 0 below 2^-6 or for a zero exponent field,
+    448 from 2^9 up or where the cut value is 480; the sign is kept."""
+    b, v = _all_bf16_finite()
+    codes = O.r2_encode(b, se)
+    L = O.lib()
+    dec = np.array([L.orc_e4m3_decode(int(c)) for c in range(256)], np.float64)[codes]
+    y = np.abs(v) * 2.0 ** -se
+    e = np.floor(np.log2(np.where(y > 0, y, 1.0)))
+    t = np.floor(y / 2.0 ** e * 8.0) / 8.0 * 2.0 ** e       # 3-bit truncation
+    want = np.where(y >= 2.0 ** -6, np.minimum(np.where(y >= 512.0, 448.0, t), 448.0), 0.0)
+    want[((b >> 7) & 0xFF) == 0] = 0.0                      # bf16 zero / subnormal
+    np.testing.assert_array_equal(np.abs(dec), want)
+    nz = codes != 0
+    np.testing.assert_array_equal((codes[nz] >> 7).astype(bool), v[nz] < 0)
+
+
+def test_r2_element_rule_equals_the_reference_integer_derivation():
+    """The reference's own second formulation (kernels/flash_attention_mx/flash_mx_impl.hpp:
+    196-216, e4m3_pack4): for P >= 0 no larger than 2^(se+1), code = t if t >= 8 else 0 with
+    t = bits[14:4] - ((120 + se) << 3), se clamped to >= -120 by its callers."""
+    b = np.arange(0, 0x7F80, dtype=np.uint32)               # +0 .. largest finite positive
+    for se in range(-120, 1):
+        keep = ((b >> 7) & 0xFF) - 127 <= se                # E <= 0: value below 2^(se+1)
+        bb = b[keep]
+        t = ((bb >> 4) & 0x7FF).astype(np.int64) - ((120 + se) << 3)
+        want = np.where(t >= 8, t, 0).astype(np.uint8)
+        np.testing.assert_array_equal(O.r2_encode(bb.astype(np.uint16), se), want)
+
+
+def test_r2_scale_maps_the_bf16_block_max_into_one_to_two():
+    L = O.lib()
+    rng = np.random.default_rng(21)
+    a = (rng.random(20000) * 2.0 ** rng.integers(-126, 1, 20000)).astype(np.float32)
+    a = a[(a >= np.float32(2.0 ** -126)) & (a <= 1)]      # normal: a subnormal max gives se = -127
+    se = np.array([L.orc_r2_scale_exp(float(x)) for x in a])
+    hb = np.array([L.orc_f32_to_bf16(float(x)) for x in a], np.uint32)
+    mb = (hb << 16).view(np.float32).astype(np.float64)
+    r = mb / 2.0 ** se
+    assert np.all((r >= 1.0) & (r < 2.0))
+    assert L.orc_r2_scale_exp(1.0) == 0 and L.orc_r2_scale_exp(0.5) == -1
+    assert L.orc_r2_scale_exp(float(np.float32(1.0 - 2.0 ** -10))) == 0   # bf16 rounds up to 1
+    assert L.orc_r2_scale_exp(float(np.float32(0.5 - 2.0 ** -12))) == -1
+    assert L.orc_r2_scale_exp(7.5) == 0                                   # clamped to <= 0
+    assert L.orc_r2_scale_exp(0.0) == -127                                # code 0
+
+
+def test_r2_blocks_target_zero():
+    """R2 over P blocks: P is rounded to bf16, each nonzero block's largest code decodes into
+    [1, 2) (the 'target-0' exponent), codes never exceed it, and an all-zero block has scale
+    and codes 0."""
+    rng = np.random.default_rng(22)
+    p = np.exp2(-rng.exponential(6.0, (512, 128))).astype(np.float32)
+    p[3] = 0.0
+    p[5, 32:64] = 0.0
+    p[7, :32] *= np.float32(2.0 ** -100)
+    pb, codes, scales = O.r2_quantize_rows(p)
+    L = O.lib()
+    hb = np.array([L.orc_f32_to_bf16(float(x)) for x in p.ravel()], np.uint32).reshape(p.shape)
+    np.testing.assert_array_equal(pb, (hb << 16).view(np.float32))
+    dec = np.array([L.orc_e4m3_decode(int(c)) for c in range(256)], np.float64)[codes]
+    blk = dec.reshape(512, 4, 32).max(axis=2)
+    nzb = pb.reshape(512, 4, 32).max(axis=2) > 0
+    assert np.all((blk[nzb] >= 1.0) & (blk[nzb] < 2.0))
+    assert np.all(scales[~nzb] == 0) and np.all(blk[~nzb] == 0)
+    assert scales[3].tolist() == [0, 0, 0, 0] and scales[5, 1] == 0
+    # dequantized P never exceeds the bf16 P and is within 2^-3 of it where not flushed
+    deq = dec * np.repeat(2.0 ** (scales.astype(np.float64) - 127), 32, axis=1)
+    assert np.all(deq <= pb)
+    kept = codes != 0
+    assert np.all(pb[kept] - deq[kept] < pb[kept] * 2.0 ** -3)
