@@ -133,6 +133,28 @@ def bench_kv_append(torch, mxfa, args):
     return out
 
 
+def bench_gemm(torch, mxfa, args):
+    """MX GEMM (mxfa_gemm) on the QKV projection of configs[2]: tokens M = B * S = 8192,
+    hidden K = Hq * D = 4096, N = (Hq + 2 Hkv) * D = 6144, E4M3 activations and weights
+    quantized on the GPU.  FLOP = 2 M N K."""
+    dev = "cuda:0"
+    M, K, N = 8192, 4096, 6144
+    X = torch.empty((M, K), dtype=torch.float32, device=dev)
+    W = torch.empty((K, N), dtype=torch.float32, device=dev)
+    mxfa.fill_normal(X, 41)
+    mxfa.fill_normal(W, 42)
+    xq, xs = mxfa.quantize_rows(X)
+    wq, ws = mxfa.quantize_cols(W)
+    xs = xs.t().contiguous()
+    del X, W
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ms = time_calls(torch, lambda: mxfa.gemm(xq, xs, wq, ws, out=c), args.steps, args.warmup)
+    tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"workload": f"QKV projection of configs[2]: M={M} N={N} K={K}, E4M3 x E4M3 -> fp32",
+            "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_call": round(ms, 4),
+            "frac_mxfp8_peak": round(tflops / MXFP8_PEAK_TFLOPS, 4)}
+
+
 def cpu_baseline(mxfa, p, ops_host, threads):
     """The CPU oracle (this repo's C restatement of the reference algorithm, threaded over
     query heads) on the whole configs[2] workload: every (batch, query head), the same
@@ -235,6 +257,7 @@ def main():
 
     if not args.no_decode:
         result["kv_append"] = bench_kv_append(torch, mxfa, args)
+        result["gemm"] = bench_gemm(torch, mxfa, args)
 
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)

@@ -167,6 +167,26 @@ mxfa_status mxfa_softmax_requant(const float *s, const float *row_max, float c, 
                                  int32_t cols, int32_t p_rule, float *p, uint8_t *codes,
                                  uint8_t *scales, float *row_sum, void *stream);
 
+/* ---- MX GEMM ---- */
+
+/* Shape and element formats of mxfa_gemm (the reference's MATMUL_M/N/K defines,
+ * kernels/gemm_mxgemmini/gen_mxgemm_data.py:105-107). */
+typedef struct {
+  int64_t m, n, k;                          /* m % 16 == 0, n % 16 == 0, k % 64 == 0 (> 0)     */
+  int32_t a_fmt, b_fmt;                     /* mxfa_fmt of the A and B element codes            */
+} mxfa_gemm_params;
+
+/* C = A x B with MX operands in the reference MX GEMM's layouts (A_in [M][K], B_in [K][N],
+ * A_scales_row [K/32][M], B_scales_col [K/32][N]; kernels/gemm_mxgemmini/gen_mxgemm_data.py:
+ * 118-126, lib/golden/mx_golden.cpp:23-30): C[m][n] = sum over 32-groups g of K of
+ * 2^(a_sc[g][m] + b_sc[g][n] - 254) * sum_{k in g} A[m][k] B[k][n], fp32 output c [M][N].
+ * Replaces the Gemmini MX GEMM driver's tile loop (lib/mxgemm/mxgemm_lib.hpp:11-250) with the
+ * scaled MXFP8 MFMA (fp32 accumulation, not Gemmini's narrow accumulators).  The reference's
+ * requant output (C_out + C_scales_row, rule R1) is mxfa_quantize_rows applied to c (scales
+ * then [M][N/32], the transpose of C_scales_row). */
+mxfa_status mxfa_gemm(const mxfa_gemm_params *p, const uint8_t *a, const uint8_t *a_sc,
+                      const uint8_t *b, const uint8_t *b_sc, float *c, void *stream);
+
 /* Synthetic inputs: x[i] ~ N(0,1) (counter-based hash + Box-Muller), each element
  * multiplied by outlier_mul with probability outlier_p.  Replaces make_inputs /
  * make_inputs_gqa (kernels/flash_attention_mx_gqa/flash_attention_model.py:58-65,166-172). */

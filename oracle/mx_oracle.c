@@ -612,3 +612,43 @@ void orc_r2_quantize_rows(const float *p, int64_t rows, int64_t cols, float *pb,
       scales[r * nb + b] = orc_r2_quantize_block(p + r * cols + b * 32, 32, pb ? pb + r * cols + b * 32 : NULL,
                                                  codes + r * cols + b * 32);
 }
+
+/* ------------------------------------------------------------------------------------
+ * MX GEMM with fp32-style (here: exact, double) accumulation: the tile semantics of the
+ * reference's MX-Gemmini GEMM (lib/mxgemm/mxgemm_lib.hpp:11-250; operand layouts of
+ * kernels/gemm_mxgemmini/gen_mxgemm_data.py:66-135 and lib/golden/mx_golden.cpp:23-30):
+ *   C[m][n] = sum_g 2^(SA[g][m] + SB[g][n] - 254) * sum_{k in g} A[m][k] * B[k][n]
+ * with A [M][K] and B [K][N] element codes, SA [K/32][M], SB [K/32][N] E8M0 codes, groups
+ * of 32 along K.  Not the Gemmini hardware accumulation (truncated products, narrow
+ * per-column accumulators, bf16 group sums) that mx_golden models.  abs_out (optional)
+ * receives sum |term| per element, the scale for error bounds.
+ * ------------------------------------------------------------------------------------ */
+void orc_mx_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                 int64_t M, int64_t N, int64_t K, int a_fmt, int b_fmt, double *c, double *abs_out) {
+  int64_t G = K / 32;
+  double *bd = malloc(sizeof(double) * K * N);
+  for (int64_t k = 0; k < K; k++)
+    for (int64_t n = 0; n < N; n++) bd[k * N + n] = orc_decode_elem(b[k * N + n], b_fmt);
+  double *ad = malloc(sizeof(double) * K);
+  for (int64_t m = 0; m < M; m++) {
+    for (int64_t k = 0; k < K; k++) ad[k] = orc_decode_elem(a[m * K + k], a_fmt);
+    for (int64_t n = 0; n < N; n++) {
+      double acc = 0.0, aacc = 0.0;
+      for (int64_t g = 0; g < G; g++) {
+        double part = 0.0, apart = 0.0;
+        for (int64_t k = 32 * g; k < 32 * g + 32; k++) {
+          double t = ad[k] * bd[k * N + n];
+          part += t;
+          apart += fabs(t);
+        }
+        double sc = ldexp(1.0, (int)sa[g * M + m] + (int)sb[g * N + n] - 254);
+        acc += part * sc;
+        aacc += apart * sc;
+      }
+      c[m * N + n] = acc;
+      if (abs_out) abs_out[m * N + n] = aacc;
+    }
+  }
+  free(bd);
+  free(ad);
+}

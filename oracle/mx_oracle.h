@@ -135,6 +135,11 @@ void    orc_r2_encode_array(const uint16_t *b, const int32_t *se, int64_t n, uin
 void    orc_r2_quantize_rows(const float *p, int64_t rows, int64_t cols, float *pb, uint8_t *codes,
                              uint8_t *scales);
 
+/* MX GEMM, exact accumulation (see mx_oracle.c): A [M][K], SA [K/32][M], B [K][N],
+ * SB [K/32][N] -> C [M][N] (double); abs_out (optional) = sum |term| per element. */
+void orc_mx_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                 int64_t M, int64_t N, int64_t K, int a_fmt, int b_fmt, double *c, double *abs_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,9 @@ def lib():
         L.orc_r2_scale_exp.argtypes = [ctypes.c_float]; L.orc_r2_scale_exp.restype = ctypes.c_int
         L.orc_r2_encode_array.argtypes = [P(ctypes.c_uint16), P(ctypes.c_int32), ctypes.c_int64, u8p]
         L.orc_r2_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, f32p, u8p, u8p]
+        f64p = P(ctypes.c_double)
+        L.orc_mx_gemm.argtypes = [u8p, u8p, u8p, u8p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                  ctypes.c_int, f64p, f64p]
         _lib = L
     return _lib
 
@@ -168,6 +171,21 @@ def r2_quantize_rows(p):
     scales = np.empty(tuple(p.shape[:-1]) + (cols // 32,), np.uint8)
     lib().orc_r2_quantize_rows(_f32(p), rows, cols, _f32(pb), _u8(codes), _u8(scales))
     return pb, codes, scales
+
+
+def mx_gemm(a, sa, b, sb, a_fmt=FMT_E4M3, b_fmt=FMT_E4M3, with_abs=False):
+    """Exact MX GEMM (float64): a [M][K], sa [K/32][M], b [K][N], sb [K/32][N] codes ->
+    C [M][N] (and sum |term| per element when with_abs)."""
+    a, sa, b, sb = (np.ascontiguousarray(x, dtype=np.uint8) for x in (a, sa, b, sb))
+    M, K = a.shape
+    N = b.shape[1]
+    assert b.shape[0] == K and K % 32 == 0 and sa.shape == (K // 32, M) and sb.shape == (K // 32, N)
+    c = np.empty((M, N), np.float64)
+    ab = np.empty((M, N), np.float64) if with_abs else None
+    f64p = ctypes.POINTER(ctypes.c_double)
+    lib().orc_mx_gemm(_u8(a), _u8(sa), _u8(b), _u8(sb), M, N, K, a_fmt, b_fmt, c.ctypes.data_as(f64p),
+                      ab.ctypes.data_as(f64p) if with_abs else None)
+    return (c, ab) if with_abs else c
 
 
 def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0, v_fmt=FMT_E4M3,

@@ -24,3 +24,17 @@ struct FaArgs {
   float sc_u;         // softmax_scale / softcap
   float cap_log2;     // softcap * log2(e) (0 = no softcap)
 };
+
+// MX GEMM kernel arguments: C [M][N] fp32 = A [M][K] x B [K][N] (element codes) with E8M0
+// scales SA [K/32][M] and SB [K/32][N].
+struct GemmArgs {
+  const uint8_t* a;
+  const uint8_t* sa;
+  const uint8_t* b;
+  const uint8_t* sb;
+  float* c;
+  int M, N, K;
+  int b_e3m2;         // B element codes are E3M2 (widened to E4M3 on the way to LDS)
+  int a_e3m2;         // A element codes are E3M2
+  int tiles_n;        // number of 128-column tiles
+};

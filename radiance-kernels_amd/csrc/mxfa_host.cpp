@@ -46,7 +46,7 @@ const char* const kKernelNames[] = {
     "mxfa_prefill_d64_r2",     "mxfa_prefill_d128_r2",    "mxfa_prefill_d256_r2",  "mxfa_prefill_d64_softcap_r2",
     "mxfa_prefill_d128_softcap_r2", "mxfa_prefill_d256_softcap_r2", "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
     "mxfa_decode_d256_r2",     "mxfa_decode_d64_softcap_r2", "mxfa_decode_d128_softcap_r2",
-    "mxfa_decode_d256_softcap_r2",
+    "mxfa_decode_d256_softcap_r2", "mxfa_gemm",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -341,6 +341,34 @@ mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, 
   int rule = p_rule;
   void* args[] = {(void*)&s, (void*)&row_max, &c, &rows, &cols_i, &p, &codes, &scales, &row_sum, &rule};
   return launch(dm, "mxfa_softmax_requant_rows", grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t* a_sc, const uint8_t* b,
+                      const uint8_t* b_sc, float* c, void* stream) {
+  if (!p) return fail(MXFA_ERR_INVALID_ARG, "params is NULL");
+  if (p->m < 1 || p->n < 1 || p->k < 1) return fail(MXFA_ERR_INVALID_ARG, "m, n and k must be >= 1");
+  if (p->k % 32) return fail(MXFA_ERR_INVALID_ARG, "k must be a multiple of 32 (scale blocks)");
+  if (p->k % 64 || p->m % 16 || p->n % 16)
+    return fail(MXFA_ERR_UNSUPPORTED, "mxfa_gemm needs k % 64 == 0, m % 16 == 0 and n % 16 == 0");
+  if (p->a_fmt != MXFA_FMT_E4M3 && p->a_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad a_fmt");
+  if (p->b_fmt != MXFA_FMT_E4M3 && p->b_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad b_fmt");
+  const int64_t lim = (int64_t)1 << 31;
+  if (p->m * p->k >= lim || p->k * p->n >= lim)
+    return fail(MXFA_ERR_UNSUPPORTED, "mxfa_gemm operands are limited to 2^31 elements");
+  const void* ptrs[] = {a, a_sc, b, b_sc, c};
+  if (mxfa_status st = check_ptrs(ptrs, 5)) return st;
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  GemmArgs g;
+  std::memset(&g, 0, sizeof g);
+  g.a = a; g.sa = a_sc; g.b = b; g.sb = b_sc; g.c = c;
+  g.M = (int)p->m; g.N = (int)p->n; g.K = (int)p->k;
+  g.a_e3m2 = p->a_fmt == MXFA_FMT_E3M2;
+  g.b_e3m2 = p->b_fmt == MXFA_FMT_E3M2;
+  const int64_t tm = (p->m + 255) / 256, tn = (p->n + 255) / 256;
+  g.tiles_n = (int)tn;
+  void* args[] = {&g};
+  return launch(dm, "mxfa_gemm", dim3((unsigned)(tm * tn)), dim3(512), args, stream);
 }
 
 mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p, float outlier_mul, void* stream) {

@@ -125,3 +125,16 @@ def test_quantize_r4_argument_validation():
     assert L.mxfa_quantize_rows_r4(None, 4, 48, None, None, None) == 1
     assert L.mxfa_quantize_rows_r4(None, 0, 64, None, None, None) == 0
     assert L.mxfa_quantize_rows_r4(None, 4, 64, None, None, None) == 1
+
+
+def test_gemm_argument_validation():
+    L = mxfa.lib()
+    G = mxfa.GemmParams
+    buf = (ctypes.c_uint8 * 64)()
+    ptr = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
+    for bad, status in ((G(0, 64, 64, 0, 0), 1), (G(64, 64, 48, 0, 0), 1), (G(64, 64, 96, 0, 0), 2),
+                        (G(40, 64, 64, 0, 0), 2), (G(64, 64, 64, 3, 0), 1), (G(1 << 20, 64, 1 << 12, 0, 0), 2)):
+        assert L.mxfa_gemm(ctypes.byref(bad), ptr, ptr, ptr, ptr, ptr, None) == status
+    ok = G(64, 64, 64, 0, 0)
+    assert L.mxfa_gemm(ctypes.byref(ok), None, ptr, ptr, ptr, ptr, None) == 1
+    assert L.mxfa_gemm(None, ptr, ptr, ptr, ptr, ptr, None) == 1
