@@ -46,7 +46,7 @@ const char* const kKernelNames[] = {
     "mxfa_prefill_d64_r2",     "mxfa_prefill_d128_r2",    "mxfa_prefill_d256_r2",  "mxfa_prefill_d64_softcap_r2",
     "mxfa_prefill_d128_softcap_r2", "mxfa_prefill_d256_softcap_r2", "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
     "mxfa_decode_d256_r2",     "mxfa_decode_d64_softcap_r2", "mxfa_decode_d128_softcap_r2",
-    "mxfa_decode_d256_softcap_r2", "mxfa_gemm",
+    "mxfa_decode_d256_softcap_r2", "mxfa_gemm", "mxfa_gemm_ae3m2", "mxfa_gemm_be3m2", "mxfa_gemm_ae3m2_be3m2",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -355,6 +355,8 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
   const int64_t lim = (int64_t)1 << 31;
   if (p->m * p->k >= lim || p->k * p->n >= lim)
     return fail(MXFA_ERR_UNSUPPORTED, "mxfa_gemm operands are limited to 2^31 elements");
+  if (p->n >= ((int64_t)1 << 22))   // a 256-row tile of C stays under 2^32 bytes
+    return fail(MXFA_ERR_UNSUPPORTED, "mxfa_gemm needs n < 4194304");
   const void* ptrs[] = {a, a_sc, b, b_sc, c};
   if (mxfa_status st = check_ptrs(ptrs, 5)) return st;
   DeviceModule* dm;
@@ -365,10 +367,12 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
   g.M = (int)p->m; g.N = (int)p->n; g.K = (int)p->k;
   g.a_e3m2 = p->a_fmt == MXFA_FMT_E3M2;
   g.b_e3m2 = p->b_fmt == MXFA_FMT_E3M2;
+  static const char* const names[2][2] = {{"mxfa_gemm", "mxfa_gemm_be3m2"},
+                                          {"mxfa_gemm_ae3m2", "mxfa_gemm_ae3m2_be3m2"}};
   const int64_t tm = (p->m + 255) / 256, tn = (p->n + 255) / 256;
   g.tiles_n = (int)tn;
   void* args[] = {&g};
-  return launch(dm, "mxfa_gemm", dim3((unsigned)(tm * tn)), dim3(512), args, stream);
+  return launch(dm, names[g.a_e3m2][g.b_e3m2], dim3((unsigned)(tm * tn)), dim3(512), args, stream);
 }
 
 mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p, float outlier_mul, void* stream) {

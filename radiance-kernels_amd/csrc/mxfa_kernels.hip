@@ -1170,88 +1170,138 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_decode_combine(FaArgs a) 
 // steps of 64 through two LDS stages; each thread stages 1/512 of the next step in
 // registers while the current one is multiplied.  A rows are read straight into the MFMA
 // row operand; B is read with ds_read_b64_tr_b8 (eight k rows of one column per lane).
-// Rows >= M and columns >= N read as zero (bounded buffer resources; N, M % 16 == 0).
+// Rows >= M and columns >= N read as zero and are not stored (bounded buffer resources;
+// M, N % 16 == 0).  The loop body is one basic block: E3M2 operands are a template
+// parameter (widened to E4M3 on the way into LDS, exact), the scale staging is spread over
+// all threads without branches, and the last step is peeled.
 // ---------------------------------------------------------------------------
 namespace gemm {
 constexpr int TM = 256, TN = 256, TK = 64;
 constexpr int AP = TK + 16;                // A row pitch in LDS (bytes)
 constexpr int BP = TN + 16;                // B row pitch (bytes)
 constexpr int A_BYTES = TM * AP, B_BYTES = TK * BP;
-constexpr int SA_BYTES = 2 * TM, SB_BYTES = 2 * TN;
+constexpr int S_BYTES = 2 * TM + 2 * TN;   // SA [2][TM] then SB [2][TN]
 constexpr int NT = 512;                    // threads per workgroup
+static_assert(TM == TN && S_BYTES == 2 * NT, "one 2-byte scale pair per thread");
 }  // namespace gemm
 
 struct GemmStage {
   v4i a[2];                                // A: 256 rows x 64 B = 1024 chunks, 2 per thread
   v4i b[2];                                // B: 64 rows x 256 B = 1024 chunks, 2 per thread
-  v4i s;                                   // scales: SA 512 B (threads 0-31), SB 512 B (32-63)
+  uint32_t s;                              // two scale codes (threads 0-255 SA, 256-511 SB)
 };
 
-__device__ __forceinline__ void gemm_load(GemmStage& r, const GemmArgs& g, int m0, int n0, int k0, int tid) {
+struct GemmRes {
+  __amdgpu_buffer_rsrc_t a;                // rows m0 .. M of A
+  int64_t soff;                            // this thread's scale row base (B offset of k0 = 0)
+  const uint8_t* sbase;                    // SA or SB (uniform per wave)
+  int sdim;                                // M or N
+  uint32_t svoff;                          // offset of the thread's pair within a k-step
+};
+
+__device__ __forceinline__ void gemm_load(GemmStage& r, const GemmArgs& g, const GemmRes& res, int n0, int k0, int tid) {
   using namespace gemm;
-  const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
   const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, (int64_t)k0 * g.N, (int64_t)TK * g.N);
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int c = tid + NT * i;
     const int row = c >> 2, col = (c & 3) * 16;                  // A chunk: row, 16-byte column
-    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, row * g.K + k0 + col, 0, 0);
+    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, row * g.K + k0 + col, 0, 0);
     const int kr = c >> 4, bc = (c & 15) * 16;                   // B chunk: k row, column
     const uint32_t bo = n0 + bc < g.N ? (uint32_t)(kr * g.N + n0 + bc) : 0x80000000u;
     r.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, bo, 0, 0);
   }
-  if (tid < 32) {                                                // SA [k0/32 + kb][m0 + 16 j ..]
-    const int kb = tid >> 4, j = tid & 15;
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g.sa, (int64_t)(k0 / 32 + kb) * g.M, g.M);
-    const uint32_t so = m0 + 16 * j < g.M ? (uint32_t)(m0 + 16 * j) : 0x80000000u;
-    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0);
-  } else if (tid < 64) {                                         // SB [k0/32 + kb][n0 + 16 j ..]
-    const int kb = (tid - 32) >> 4, j = tid & 15;
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g.sb, (int64_t)(k0 / 32 + kb) * g.N, g.N);
-    const uint32_t so = n0 + 16 * j < g.N ? (uint32_t)(n0 + 16 * j) : 0x80000000u;
-    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0);
-  }
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, 2 * (int64_t)res.sdim);
+  r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, res.svoff, 0, 0);
 }
 
-__device__ __forceinline__ void gemm_store(const GemmStage& r, uint8_t* sA, uint8_t* sB, uint8_t* sSA, uint8_t* sSB,
-                                           int tid, int a_e3m2, int b_e3m2) {
+template <int AE3, int BE3>
+__device__ __forceinline__ void gemm_store(const GemmStage& r, uint8_t* sA, uint8_t* sB, uint8_t* sS, int tid) {
   using namespace gemm;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int c = tid + NT * i;
     v4i va = r.a[i], vb = r.b[i];
-    if (a_e3m2) {
+    if (AE3) {
 #pragma unroll
       for (int w = 0; w < 4; w++) va[w] = (int)e3m2x4_to_e4m3x4((uint32_t)va[w]);
     }
-    if (b_e3m2) {
+    if (BE3) {
 #pragma unroll
       for (int w = 0; w < 4; w++) vb[w] = (int)e3m2x4_to_e4m3x4((uint32_t)vb[w]);
     }
     *reinterpret_cast<v4i*>(sA + (c >> 2) * AP + (c & 3) * 16) = va;
     *reinterpret_cast<v4i*>(sB + (c >> 4) * BP + (c & 15) * 16) = vb;
   }
-  if (tid < 32)
-    *reinterpret_cast<v4i*>(sSA + (tid >> 4) * TM + (tid & 15) * 16) = r.s;
-  else if (tid < 64)
-    *reinterpret_cast<v4i*>(sSB + ((tid - 32) >> 4) * TN + (tid & 15) * 16) = r.s;
+  *reinterpret_cast<uint16_t*>(sS + 2 * tid) = (uint16_t)r.s;
 }
 
-extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm(GemmArgs g) {
+// One k-step of the wave's 4 x 2 MFMA tiles from one LDS stage.
+__device__ __forceinline__ void gemm_mma(v16f (&acc)[4][2], const uint8_t* sA, const uint8_t* sB, const uint8_t* sS,
+                                         int wr, int wc, int lane) {
+  using namespace gemm;
+  const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
+  // operands: A row tile i (rows 128 wr + 32 i + r, k = 16 h .. and 32 + 16 h ..), B
+  // column tile j (column 64 wc + 32 j + 16 (g16 & 1) + l16, k rows via transposed reads)
+  v8i bo[2];
+  int bsc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int ncol = 64 * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int krow = 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
+      v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB + krow * BP + ncol));
+      bo[j][2 * q] = t[0];
+      bo[j][2 * q + 1] = t[1];
+    }
+    bsc[j] = sS[2 * TM + h * TN + 64 * wc + 32 * j + r];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = 128 * wr + 32 * i + r;
+    const v4i lo = *reinterpret_cast<const v4i*>(sA + row * AP + 16 * h);
+    const v4i hi = *reinterpret_cast<const v4i*>(sA + row * AP + 32 + 16 * h);
+    const v8i ao = cat44(lo, hi);
+    const int asc = sS[h * TM + row];
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
+  }
+}
+
+template <int AE3, int BE3>
+__device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
   using namespace gemm;
   __shared__ __attribute__((aligned(16))) uint8_t sA[2][A_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2][B_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t sSA[2][SA_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t sSB[2][SB_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t sS[2][S_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
-  // XCD-aware order: consecutive tiles of one XCD share rows of A (see prefill_impl)
+  // XCD-aware grouped order.  Workgroup lin runs on XCD lin % 8, which takes a contiguous
+  // run of tile indices; tiles are numbered in groups of GM tile rows, column by column
+  // inside a group, so the 32 tiles one XCD holds at a time form a 4 x 8 block of C and
+  // its L2 sees 4 A panels and 8 B panels per k-step (row-major order: 2 and 24).
+  constexpr int GM = 4;
   const int nwg = (int)gridDim.x, lin = (int)blockIdx.x;
   const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
   const int item = xcd * per + min(xcd, rem) + (lin >> 3);
-  const int m0 = (item / g.tiles_n) * TM, n0 = (item % g.tiles_n) * TN;
+  const int tiles_m = (g.M + TM - 1) / TM;
+  const int group = item / (GM * g.tiles_n), first = group * GM, gm = min(GM, tiles_m - first);
+  const int in_group = item - group * GM * g.tiles_n;
+  const int m0 = (first + in_group % gm) * TM, n0 = (in_group / gm) * TN;
   const int wr = wave >> 2, wc = wave & 3;
+
+  GemmRes res;
+  res.a = buf_rsrc(g.a, (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
+  {
+    // thread t stages scale codes [k0/32 + kb][c0 + 2 cp ..+2] of SA (t < 256) or SB
+    const bool is_a = wave < 4;
+    const int t = tid & 255, kb = t >> 7, cp = t & 127;
+    res.sbase = is_a ? g.sa : g.sb;
+    res.sdim = is_a ? g.M : g.N;
+    const int c = (is_a ? m0 : n0) + 2 * cp;
+    res.svoff = c < res.sdim ? (uint32_t)(kb * res.sdim + c) : 0x80000000u;
+  }
 
   v16f acc[4][2];
 #pragma unroll
@@ -1261,53 +1311,44 @@ extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm(GemmArgs g) {
 
   const int nk = g.K / TK;
   GemmStage st;
-  gemm_load(st, g, m0, n0, 0, tid);
-  gemm_store(st, sA[0], sB[0], sSA[0], sSB[0], tid, g.a_e3m2, g.b_e3m2);
+  gemm_load(st, g, res, n0, 0, tid);
+  gemm_store<AE3, BE3>(st, sA[0], sB[0], sS[0], tid);
   __syncthreads();
-  for (int kt = 0; kt < nk; kt++) {
+  for (int kt = 0; kt < nk - 1; kt++) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) gemm_load(st, g, m0, n0, (kt + 1) * TK, tid);
-    // operands: A row tile i (rows 128 wr + 32 i + r, k = 16 h .. and 32 + 16 h ..), B
-    // column tile j (column 64 wc + 32 j + 16 (g16 & 1) + l16, k rows via transposed reads)
-    v8i bo[2];
-    int bsc[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int ncol = 64 * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int krow = 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
-        v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB[buf] + krow * BP + ncol));
-        bo[j][2 * q] = t[0];
-        bo[j][2 * q + 1] = t[1];
-      }
-      bsc[j] = sSB[buf][h * TN + 64 * wc + 32 * j + r];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = 128 * wr + 32 * i + r;
-      const v4i lo = *reinterpret_cast<const v4i*>(sA[buf] + row * AP + 16 * h);
-      const v4i hi = *reinterpret_cast<const v4i*>(sA[buf] + row * AP + 32 + 16 * h);
-      const v8i ao = cat44(lo, hi);
-      const int asc = sSA[buf][h * TM + row];
-#pragma unroll
-      for (int j = 0; j < 2; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
-    }
-    if (kt + 1 < nk) gemm_store(st, sA[buf ^ 1], sB[buf ^ 1], sSA[buf ^ 1], sSB[buf ^ 1], tid, g.a_e3m2, g.b_e3m2);
+    // the next step's loads go out first and the MFMAs before their wait (the scheduler
+    // otherwise sinks the loads between the MFMAs to save registers)
+    gemm_load(st, g, res, n0, (kt + 1) * TK, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    gemm_mma(acc, sA[buf], sB[buf], sS[buf], wr, wc, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    gemm_store<AE3, BE3>(st, sA[buf ^ 1], sB[buf ^ 1], sS[buf ^ 1], tid);
     __syncthreads();
   }
+  gemm_mma(acc, sA[(nk - 1) & 1], sB[(nk - 1) & 1], sS[(nk - 1) & 1], wr, wc, lane);
 
   // C tile: lane l, register v of tile (i, j) -> row 128 wr + 32 i + 8 (v / 4) + 4 h + v % 4,
-  // column 64 wc + 32 j + r
+  // column 64 wc + 32 j + r.  Rows >= M fall outside the tile's resource; columns >= N get
+  // an offset outside every resource.
+  const int r = lane & 31, h = lane >> 5;
+  const int rows = min(TM, g.M - m0);
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.c + (int64_t)m0 * g.N), 0, (int)(uint32_t)((int64_t)rows * g.N * 4), 0x00020000);
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int j = 0; j < 2; j++) {
+    const int n = n0 + 64 * wc + 32 * j + r;
+    const uint32_t cb = n < g.N ? (uint32_t)((128 * wr + 4 * h) * g.N + n) * 4u : 0xfffffff0u;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int n = n0 + 64 * wc + 32 * j + r;
+    for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const int m = m0 + 128 * wr + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < g.M && n < g.N) g.c[(int64_t)m * g.N + n] = acc[i][j][v];
+        const uint32_t off = n < g.N ? cb + (uint32_t)((32 * i + 8 * (v >> 2) + (v & 3)) * g.N) * 4u : cb;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), rc, off, 0, 0);
       }
-    }
+  }
 }
+
+extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm(GemmArgs g) { gemm_impl<0, 0>(g); }
+extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_ae3m2(GemmArgs g) { gemm_impl<1, 0>(g); }
+extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_be3m2(GemmArgs g) { gemm_impl<0, 1>(g); }
+extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_ae3m2_be3m2(GemmArgs g) { gemm_impl<1, 1>(g); }

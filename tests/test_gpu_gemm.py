@@ -53,6 +53,7 @@ def test_gemm_matches_oracle(M, N, K):
 def test_gemm_e3m2_operands_and_wide_scales():
     run_gemm(256, 128, 512, seed=11, a_fmt=mxfa.FMT_E3M2)
     run_gemm(128, 256, 256, seed=12, b_fmt=mxfa.FMT_E3M2)
+    run_gemm(144, 336, 384, seed=14, a_fmt=mxfa.FMT_E3M2, b_fmt=mxfa.FMT_E3M2)
     # scale sums 2^-94 .. 2^84: every product and sum stays in fp32's normal range
     run_gemm(128, 128, 256, seed=13, srange=(80, 170))
 
