@@ -176,13 +176,11 @@ const char* kernel_name(const char* kind, const mxfa_attn_params* p) {
   return buf;
 }
 
-// Decode geometry: chunks of split_len keys (multiple of 64) so that the whole
-// call has about 16K waves in flight.
 // Split-KV plan: chunks of split_len keys (a multiple of 64) so that about kDecodeWaves
-// chunk waves cover the cache -- about 1.5 waves per decode wave slot of the 256-CU chip
-// (8 per CU): one round of long chunks, few partials to merge (measured on MI355X:
-// 16384 waves 4.7 TB/s, 2048 5.3, 1536 5.4).  MXFA_DECODE_WAVES overrides the target.
-constexpr int64_t kDecodeWaves = 1536;
+// chunk waves cover the cache -- one wave per SIMD of the 256-CU chip: one round of long
+// chunks, each wave keeping the next block's K and V in flight, few partials to merge.
+// MXFA_DECODE_WAVES overrides the target.
+constexpr int64_t kDecodeWaves = 1024;
 
 int64_t decode_wave_target() {
   if (const char* env = getenv("MXFA_DECODE_WAVES")) {
@@ -434,8 +432,12 @@ mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8
   int64_t nbh = (int64_t)p->batch * p->num_q_heads;
   a.part_o = reinterpret_cast<float*>(workspace);
   a.part_ml = a.part_o + nbh * nparts * p->head_dim;
-  const int nw = p->head_dim == 256 ? 2 : 4;   // waves per decode workgroup (LDS-limited at D = 256)
-  dim3 grid((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads));
+  // D <= 128: 4 waves per workgroup over the linear (b, KV head, chunk) items; D = 256:
+  // 2 waves (LDS-limited) over the chunks of one (b, KV head) per grid row
+  const int nw = p->head_dim == 256 ? 2 : 4;
+  const int64_t items = (int64_t)p->batch * p->num_kv_heads * nparts;
+  dim3 grid = p->head_dim == 256 ? dim3((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads))
+                                 : dim3((unsigned)((items + nw - 1) / nw));
   void* args[] = {&a};
   if (mxfa_status st = launch(dm, kernel_name("decode", p), grid, dim3(64 * nw), args, stream))
     return st;

@@ -917,9 +917,11 @@ __device__ void decode_split_impl(const FaArgs& a) {
   __shared__ __attribute__((aligned(16))) uint8_t sVs[NW][Lds<D>::SC];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
-  const int part = blockIdx.x * NW + wave;
-  const int bk = blockIdx.y;
-  if (part >= a.n_qblk) return;                       // waves past the last chunk have no work
+  // one (batch, KV head, chunk) item per wave, items numbered chunk-fastest over the
+  // whole grid: every wave of a workgroup has work (the waves share nothing)
+  const int item = blockIdx.x * NW + wave;
+  if (item >= a.B * a.Hkv * a.n_qblk) return;         // waves past the last item have no work
+  const int bk = item / a.n_qblk, part = item - bk * a.n_qblk;
   const int b = bk / a.Hkv, kvh = bk % a.Hkv;
   const bool qvalid = r < a.group;
   const int head = kvh * a.group + (qvalid ? r : 0);
@@ -940,6 +942,14 @@ __device__ void decode_split_impl(const FaArgs& a) {
   int klo, khi;
   key_limits(a, qpos, qvalid, klo, khi);
   khi = min(khi, kend - 1);                          // the rest of the tile belongs to other chunks
+  // The visible range of the (single) query position, uniform over the wave: blocks
+  // outside it contribute nothing (P = 0, the max unchanged) and are not visited; blocks
+  // inside it need no mask.  Padding columns (r >= group, Q = 0) are not masked: their
+  // scores are 0, their state stays finite and is never written.
+  int klo_u, khi_u;
+  key_limits(a, qpos, true, klo_u, khi_u);
+  khi_u = min(khi_u, kend - 1);
+  const int kfirst = max(kbeg, klo_u & ~(BN - 1)), klast = min(kend, khi_u + 1);
 
   WaveState<D> st;
 #pragma unroll
@@ -947,40 +957,43 @@ __device__ void decode_split_impl(const FaArgs& a) {
   st.m = -INFINITY;
   st.l = 0.0f;
 
-  for (int key0 = kbeg; key0 < kend; key0 += BN) {
-    // this lane's K half-rows (keys key0 + 32t + r) and their E8M0 scales
-    v4i kr[NT][KC];
-    uint32_t ksr[NT];
+  // this lane's K half-rows (keys key0 + 32t + r) and their E8M0 scales
+  v4i kr[NT][KC];
+  uint32_t ksr[NT];
+  // (a disabled load gets an offset past every resource: it reads nothing and returns 0;
+  // no branch, so the waits on the other loads stay partial)
+  auto load_k = [&](int key0, bool on) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       const int row = key0 + 32 * t + r;
+      const uint32_t ko = on ? (uint32_t)(row * D + h * (D / 2)) : 0x80000000u;
+      const uint32_t so = on ? (uint32_t)(D == 128 ? row * 4 + 2 * h : row * 2 + h) : 0x80000000u;
 #pragma unroll
-      for (int c = 0; c < KC; c++)
-        kr[t][c] = __builtin_amdgcn_raw_buffer_load_b128(rk, row * D + h * (D / 2) + 16 * c, 0, 0);
+      for (int c = 0; c < KC; c++) kr[t][c] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * c, 0, 0);
       if constexpr (D == 128)
-        ksr[t] = __builtin_amdgcn_raw_buffer_load_b16(rks, row * 4 + 2 * h, 0, 0);
+        ksr[t] = __builtin_amdgcn_raw_buffer_load_b16(rks, so, 0, 0);
       else
-        ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, row * 2 + h, 0, 0);
+        ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, so, 0, 0);
     }
-    // V codes and scales -> the wave's LDS slot (E3M2 widened to E4M3)
-    v4i vr[PERW];
+  };
+  // V codes and scales of a block (stored to the wave's LDS slot after its scores)
+  v4i vr[PERW];
+  uint32_t vsr;
+  auto load_v = [&](int key0, bool on) {
 #pragma unroll
     for (int i = 0; i < PERW; i++) {
       const int c = lane + 64 * i;
-      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, (key0 + c / CPR) * D + (c % CPR) * 16, 0, 0);
+      const uint32_t vo = on ? (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16) : 0x80000000u;
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0);
     }
-    const uint32_t vsr = lane < SCW ? __builtin_amdgcn_raw_buffer_load_b32(rvs, (key0 / 32) * D + 4 * lane, 0, 0) : 0u;
-#pragma unroll
-    for (int i = 0; i < PERW; i++) {
-      const int c = lane + 64 * i;
-      v4i zv = vr[i];
-      if (a.v_e3m2) {
-#pragma unroll
-        for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
-      }
-      *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = zv;
-    }
-    if (lane < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * lane]) = vsr;
+    const uint32_t so = on && lane < SCW ? (uint32_t)((key0 / 32) * D + 4 * lane) : 0x80000000u;
+    vsr = __builtin_amdgcn_raw_buffer_load_b32(rvs, so, 0, 0);
+  };
+  // one block ahead: K(j+1) goes out after the scores of block j, V(j+1) after V(j) is in
+  // LDS, and both stay in flight through the softmax and PV of block j
+  load_k(kfirst, kfirst < klast);
+  load_v(kfirst, kfirst < klast);
+  for (int key0 = kfirst; key0 < klast; key0 += BN) {
     // scores from registers: K dequantized to bf16 just before each MFMA
     v16f sc[NT];
 #pragma unroll
@@ -994,9 +1007,23 @@ __device__ void decode_split_impl(const FaArgs& a) {
         sc[t] = mfma_bf16(ka, qb[kk], sc[t]);
       }
     }
+    load_k(key0 + BN, key0 + BN < klast);
+#pragma unroll
+    for (int i = 0; i < PERW; i++) {
+      const int c = lane + 64 * i;
+      v4i zv = vr[i];
+      if (a.v_e3m2) {
+#pragma unroll
+        for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
+      }
+      *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = zv;
+    }
+    if (lane < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * lane]) = vsr;
+    load_v(key0 + BN, key0 + BN < klast);
     // LDS operations of one wave complete in order: the V tile written above is in place
     // for the transposed reads, and the next block's writes follow this block's reads
-    softmax_pv<D, SOFTCAP, PR>(st, sc, sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
+    const bool mask = key0 < klo_u || key0 + BN - 1 > khi_u;
+    softmax_pv<D, SOFTCAP, PR>(st, sc, sV[wave], sVs[wave], key0, klo, khi, mask, a, lane);
   }
 
   // partial outputs (unnormalized O, m in x units, full l)
