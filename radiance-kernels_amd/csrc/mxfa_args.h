@@ -20,6 +20,7 @@ struct FaArgs {
   int qpw;            // prefill: query positions per workgroup
   int n_qblk;         // prefill: query blocks; decode: number of partials per query head
   int split_len;      // decode: keys per partial (multiple of 64)
+  int fuse_combine;   // decode (D <= 128): the chunks of a head merge inside the workgroup
   float c_log2;       // softmax_scale * log2(e)  (no softcap)
   float sc_u;         // softmax_scale / softcap
   float cap_log2;     // softcap * log2(e) (0 = no softcap)

@@ -438,9 +438,18 @@ mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8
   const int64_t items = (int64_t)p->batch * p->num_kv_heads * nparts;
   dim3 grid = p->head_dim == 256 ? dim3((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads))
                                  : dim3((unsigned)((items + nw - 1) / nw));
+  // When every head's chunks fit in one workgroup (nparts divides its 4 waves) and the
+  // valid columns' partials fit the waves' V slots (group <= 16), the kernel merges them
+  // itself (same formula and order as mxfa_decode_combine) and no combine launch follows.
+  // MXFA_DECODE_COMBINE=kernel selects the combine kernel always (the two paths give
+  // bit-identical O; the switch exists to test exactly that).
+  const char* comb = getenv("MXFA_DECODE_COMBINE");
+  const bool force_kernel = comb && std::strcmp(comb, "kernel") == 0;
+  a.fuse_combine = !force_kernel && p->head_dim <= 128 && nw % nparts == 0 && a.group <= 16;
   void* args[] = {&a};
   if (mxfa_status st = launch(dm, kernel_name("decode", p), grid, dim3(64 * nw), args, stream))
     return st;
+  if (a.fuse_combine) return MXFA_OK;
   return launch(dm, "mxfa_decode_combine", dim3((unsigned)nbh), dim3((unsigned)p->head_dim), args, stream);
 }
 

@@ -919,9 +919,14 @@ __device__ void decode_split_impl(const FaArgs& a) {
   const int r = lane & 31, h = lane >> 5;
   // one (batch, KV head, chunk) item per wave, items numbered chunk-fastest over the
   // whole grid: every wave of a workgroup has work (the waves share nothing)
+  // Waves past the last item have no work; they stay for the workgroup barrier of the
+  // fused merge below (their loads use the last item's addresses and read nothing).
+  const int n_items = a.B * a.Hkv * a.n_qblk;
   const int item = blockIdx.x * NW + wave;
-  if (item >= a.B * a.Hkv * a.n_qblk) return;         // waves past the last item have no work
-  const int bk = item / a.n_qblk, part = item - bk * a.n_qblk;
+  const bool active = item < n_items;
+  if (!active && !a.fuse_combine) return;
+  const int it = active ? item : n_items - 1;
+  const int bk = it / a.n_qblk, part = it - bk * a.n_qblk;
   const int b = bk / a.Hkv, kvh = bk % a.Hkv;
   const bool qvalid = r < a.group;
   const int head = kvh * a.group + (qvalid ? r : 0);
@@ -949,7 +954,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
   int klo_u, khi_u;
   key_limits(a, qpos, true, klo_u, khi_u);
   khi_u = min(khi_u, kend - 1);
-  const int kfirst = max(kbeg, klo_u & ~(BN - 1)), klast = min(kend, khi_u + 1);
+  const int kfirst = max(kbeg, klo_u & ~(BN - 1)), klast = active ? min(kend, khi_u + 1) : kfirst;
 
   WaveState<D> st;
 #pragma unroll
@@ -1026,9 +1031,73 @@ __device__ void decode_split_impl(const FaArgs& a) {
     softmax_pv<D, SOFTCAP, PR>(st, sc, sV[wave], sVs[wave], key0, klo, khi, mask, a, lane);
   }
 
-  // partial outputs (unnormalized O, m in x units, full l)
   float l = pair_sum(st.l);
   const int nparts = a.n_qblk;
+  if (a.fuse_combine) {
+    // All chunks of a (b, KV head) are waves of this workgroup (nparts divides NW, group
+    // <= 16).  Every wave leaves (O, m, l) of its valid columns in its own (now unused)
+    // LDS slot; then all threads merge: each takes 4 consecutive d of one query head and
+    // combines the chunks in chunk order with the formula of mxfa_decode_combine.
+    const int G = a.group;
+    float* po = reinterpret_cast<float*>(sV[wave]);
+    float* pml = reinterpret_cast<float*>(sVs[wave]);
+    // slot layout: float4 (dt, g) of column (h, r) at [(dt * 4 + g) * 2G + h G + r]
+    if (active && qvalid) {
+#pragma unroll
+      for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          reinterpret_cast<float4*>(po)[(dt * 4 + g) * 2 * G + h * G + r] =
+              make_float4(st.o[dt][4 * g], st.o[dt][4 * g + 1], st.o[dt][4 * g + 2], st.o[dt][4 * g + 3]);
+      if (h == 0) {
+        pml[2 * r] = st.m;
+        pml[2 * r + 1] = l;
+      }
+    }
+    __syncthreads();
+    const float c = SOFTCAP ? 1.0f : a.c_log2;
+    const int heads_wg = NW / nparts, per_head = G * (D / 4);
+    for (int u = tid; u < heads_wg * per_head; u += 64 * NW) {
+      const int hg = u / per_head, rem = u - hg * per_head;
+      const int q = rem / (D / 4), d = 4 * (rem - q * (D / 4));
+      const int item0 = blockIdx.x * NW + hg * nparts;
+      if (item0 >= n_items) break;
+      const int bk0 = item0 / nparts;
+      // register position of d: dt = d / 32, g = (d % 32) / 8, half = (d % 8) / 4
+      const int fi = ((d >> 5) * 4 + ((d & 31) >> 3)) * 2 * G + ((d & 7) >> 2) * G + q;
+      float M = -INFINITY;
+      for (int i = 0; i < nparts; i++) {
+        const float* qml = reinterpret_cast<const float*>(sVs[hg * nparts + i]);
+        if (qml[2 * q + 1] > 0.0f) M = fmaxf(M, qml[2 * q]);
+      }
+      float L = 0.0f;
+      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (M != -INFINITY) {
+        const float mc = M * c;
+        for (int i = 0; i < nparts; i++) {
+          const float* qml = reinterpret_cast<const float*>(sVs[hg * nparts + i]);
+          const float li = qml[2 * q + 1];
+          if (!(li > 0.0f)) continue;
+          const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(qml[2 * q], c, -mc));
+          L += li * w;
+          const float4 o4 = reinterpret_cast<const float4*>(sV[hg * nparts + i])[fi];
+          acc.x += o4.x * w;
+          acc.y += o4.y * w;
+          acc.z += o4.z * w;
+          acc.w += o4.w * w;
+        }
+      }
+      float4 v;
+      v.x = L > 0.0f ? acc.x / L : 0.0f;
+      v.y = L > 0.0f ? acc.y / L : 0.0f;
+      v.z = L > 0.0f ? acc.z / L : 0.0f;
+      v.w = L > 0.0f ? acc.w / L : 0.0f;
+      const int b0 = bk0 / a.Hkv, kv0 = bk0 % a.Hkv;
+      *reinterpret_cast<float4*>(a.o + ((int64_t)b0 * a.Hq + kv0 * G + q) * D + d) = v;
+    }
+    return;
+  }
+  // partial outputs (unnormalized O, m in x units, full l) for mxfa_decode_combine
   if (qvalid) {
     float* po = a.part_o + (bh * nparts + part) * D;
 #pragma unroll

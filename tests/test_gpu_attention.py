@@ -148,6 +148,35 @@ def test_decode_config5_sampled():
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,waves,window,softcap", [
+    (4, 32, 8, 1024, 128, 32, 0, 0.0),        # 1 chunk per head
+    (4, 32, 8, 1024, 128, 64, 0, 0.0),        # 2 chunks
+    (4, 32, 8, 1024, 128, 128, 300, 0.0),     # 4 chunks, window (leading chunks skip blocks)
+    (3, 8, 2, 480, 64, 24, 0, 30.0),          # 4 ragged chunks, softcap, D = 64
+    (2, 64, 4, 1056, 128, 16, 0, 0.0),        # group 16, ragged last block
+    (4, 32, 8, 1024, 128, 96, 0, 0.0),        # 3 chunks: not fused, both runs use the kernel
+])
+def test_decode_fused_merge_matches_combine_kernel(monkeypatch, B, Hq, Hkv, L, D, waves, window, softcap):
+    """The in-workgroup merge of the chunk partials (one launch) and mxfa_decode_combine
+    (two launches) give bit-identical O: same partials, same formula, same chunk order."""
+    print(f"decode fused-vs-kernel B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} waves {waves}", flush=True)
+    monkeypatch.setenv("MXFA_DECODE_WAVES", str(waves))
+    fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L, D, seed=40 + waves)
+    p = mxfa.make_params(B, Hq, Hkv, 1, L, D, causal=True, q_pos0=L - 1, window=window, softcap=softcap)
+    args = (p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
+    fused = mxfa.decode(*args)
+    monkeypatch.setenv("MXFA_DECODE_COMBINE", "kernel")
+    combined = mxfa.decode(*args)
+    torch.cuda.synchronize()
+    assert torch.isfinite(fused).all()
+    assert torch.equal(fused, combined)
+    split_len, _ = mxfa.decode_plan(p)
+    want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
+                       block_n=mxfa.DEFAULT_BLOCK_N, split_len=split_len)
+    rel, mab = errors(np_(fused), want)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+
+
 # ---- P rule R2: the reference device kernels' truncating "target-0" requant of bf16 P
 # (kernels/flash_attention_mx_gqa/flash_mx_impl.hpp:53-77, 366-388), same tolerance
 # against the oracle run with the same rule.
