@@ -1295,19 +1295,22 @@ struct GemmRes {
   uint32_t svoff;                          // offset of the thread's pair within a k-step
 };
 
+// Loads of a step at k0 >= K read nothing and return zeros (E8M0 code 0 = 2^-127 scales,
+// so that step adds exact zeros).
 __device__ __forceinline__ void gemm_load(GemmStage& r, const GemmArgs& g, const GemmRes& res, int n0, int k0, int tid) {
   using namespace gemm;
-  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, (int64_t)k0 * g.N, (int64_t)TK * g.N);
+  const bool on = k0 < g.K;
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, (int64_t)k0 * g.N, on ? (int64_t)TK * g.N : 0);
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int c = tid + NT * i;
     const int row = c >> 2, col = (c & 3) * 16;                  // A chunk: row, 16-byte column
-    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, row * g.K + k0 + col, 0, 0);
+    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, on ? (uint32_t)(row * g.K + k0 + col) : 0x80000000u, 0, 0);
     const int kr = c >> 4, bc = (c & 15) * 16;                   // B chunk: k row, column
     const uint32_t bo = n0 + bc < g.N ? (uint32_t)(kr * g.N + n0 + bc) : 0x80000000u;
     r.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, bo, 0, 0);
   }
-  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, 2 * (int64_t)res.sdim);
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, on ? 2 * (int64_t)res.sdim : 0);
   r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, res.svoff, 0, 0);
 }
 
@@ -1405,23 +1408,31 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = (v16f){};
 
+  // Two register stages: step k + 2 is loaded while step k is multiplied and step k + 1
+  // (loaded one step earlier) goes into the other LDS stage.  The loop runs steps in
+  // pairs; for odd K / 64 the last step multiplies zeros.
   const int nk = g.K / TK;
-  GemmStage st;
-  gemm_load(st, g, res, n0, 0, tid);
-  gemm_store<AE3, BE3>(st, sA[0], sB[0], sS[0], tid);
+  GemmStage s0, s1;
+  gemm_load(s0, g, res, n0, 0, tid);
+  gemm_load(s1, g, res, n0, TK, tid);
+  gemm_store<AE3, BE3>(s0, sA[0], sB[0], sS[0], tid);
   __syncthreads();
-  for (int kt = 0; kt < nk - 1; kt++) {
-    const int buf = kt & 1;
-    // the next step's loads go out first and the MFMAs before their wait (the scheduler
+  for (int kt = 0; kt < nk; kt += 2) {
+    // loads go out first and the MFMAs before the wait of the stores (the scheduler
     // otherwise sinks the loads between the MFMAs to save registers)
-    gemm_load(st, g, res, n0, (kt + 1) * TK, tid);
+    gemm_load(s0, g, res, n0, (kt + 2) * TK, tid);
     __builtin_amdgcn_sched_barrier(0);
-    gemm_mma(acc, sA[buf], sB[buf], sS[buf], wr, wc, lane);
+    gemm_mma(acc, sA[0], sB[0], sS[0], wr, wc, lane);
     __builtin_amdgcn_sched_barrier(0);
-    gemm_store<AE3, BE3>(st, sA[buf ^ 1], sB[buf ^ 1], sS[buf ^ 1], tid);
+    gemm_store<AE3, BE3>(s1, sA[1], sB[1], sS[1], tid);
+    __syncthreads();
+    gemm_load(s1, g, res, n0, (kt + 3) * TK, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    gemm_mma(acc, sA[1], sB[1], sS[1], wr, wc, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    gemm_store<AE3, BE3>(s0, sA[0], sB[0], sS[0], tid);
     __syncthreads();
   }
-  gemm_mma(acc, sA[(nk - 1) & 1], sB[(nk - 1) & 1], sS[(nk - 1) & 1], wr, wc, lane);
 
   // C tile: lane l, register v of tile (i, j) -> row 128 wr + 32 i + 8 (v / 4) + 4 h + v % 4,
   // column 64 wc + 32 j + r.  Rows >= M fall outside the tile's resource; columns >= N get
