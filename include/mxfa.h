@@ -114,10 +114,11 @@ mxfa_status mxfa_prefill(const mxfa_attn_params *p,
                          float *o, void *stream);
 
 /* Split-KV decode plan for seq_q == 1 (q_pos0 is the query's position, normally
- * seq_k - 1): keys are processed in independent chunks of *split_len keys (each a
- * streaming pass with block_n-key blocks) merged by log-sum-exp.  The reference has
- * no decode kernel; this is the same recurrence over a KV cache. */
-mxfa_status mxfa_decode_plan(const mxfa_attn_params *p, int32_t *split_len, size_t *workspace_bytes);
+ * seq_k - 1): the 64-key blocks are dealt to *n_parts independent partials (partial i
+ * takes blocks i, i + n_parts, ...; each a streaming pass) merged in order by
+ * log-sum-exp.  The reference has no decode kernel; this is the same recurrence over a
+ * KV cache. */
+mxfa_status mxfa_decode_plan(const mxfa_attn_params *p, int32_t *n_parts, size_t *workspace_bytes);
 
 mxfa_status mxfa_decode(const mxfa_attn_params *p,
                         const uint8_t *q, const uint8_t *q_sc,

@@ -230,7 +230,7 @@ typedef struct {
   const orc_attn_params *p;
   const uint8_t *q, *q_sc, *k, *k_sc, *v, *v_sc;
   float *o;
-  int block_n, split_len, dense;
+  int block_n, split_len, n_parts, dense;
   const int32_t *heads;
   int nheads;
   double **kd, **vd;         /* dequantized K/V per flattened kv head (NULL if unused) */
@@ -269,13 +269,15 @@ static double score_of(const orc_attn_params *p, const double *qd, const double 
 
 /* One streaming pass over keys [k0, k1) with blocks aligned to block_n.
  * Outputs unnormalized O, running max m and sum l. */
+/* One streaming pass over the key blocks starting at k0, k0 + stride, ... below k1; each
+ * block is [b0, min(b0 + block_n, k1)).  stride = block_n: the keys [k0, k1) in order. */
 static void flash_pass(const orc_attn_params *p, const double *qd, const double *kd, const double *vd,
-                       int64_t qpos, int64_t k0, int64_t k1, int block_n,
+                       int64_t qpos, int64_t k0, int64_t k1, int block_n, int64_t stride,
                        double *O, double *m_out, double *l_out, double *S, float *P) {
   int D = p->head_dim;
   double m = -INFINITY, l = 0.0;
   for (int d = 0; d < D; d++) O[d] = 0.0;
-  for (int64_t b0 = k0; b0 < k1; b0 += block_n) {
+  for (int64_t b0 = k0; b0 < k1; b0 += stride) {
     int64_t b1 = b0 + block_n < k1 ? b0 + block_n : k1;
     int n = (int)(b1 - b0);
     double bmax = -INFINITY;
@@ -345,14 +347,22 @@ static void do_row(job_t *J, int64_t bh, int64_t i, double *qd, double *O, doubl
     for (int64_t d = 0; d < D; d++) out[d] = l > 0.0 ? (float)(O[d] / l) : 0.0f;
     return;
   }
+  /* partials: n_parts > 0 -- partial i takes the key blocks i, i + n_parts, i + 2 n_parts,
+   * ... (the interleaved decode schedule); else contiguous chunks of split_len keys (one
+   * chunk when 0).  Partials are merged in order by log-sum-exp. */
   int64_t Sk = p->seq_k;
   int64_t chunk = J->split_len > 0 ? J->split_len : Sk;
+  int64_t nparts = J->n_parts > 0 ? J->n_parts : (Sk + chunk - 1) / chunk;
   double M = -INFINITY, L = 0.0;
   for (int64_t d = 0; d < D; d++) O[d] = 0.0;
-  for (int64_t c0 = 0; c0 < Sk; c0 += chunk) {
-    int64_t c1 = c0 + chunk < Sk ? c0 + chunk : Sk;
+  for (int64_t i = 0; i < nparts; i++) {
     double mc, lc;
-    flash_pass(p, qd, kd, vd, qpos, c0, c1, J->block_n, Oc, &mc, &lc, S, P);
+    if (J->n_parts > 0)
+      flash_pass(p, qd, kd, vd, qpos, i * J->block_n, Sk, J->block_n, (int64_t)J->n_parts * J->block_n, Oc, &mc,
+                 &lc, S, P);
+    else
+      flash_pass(p, qd, kd, vd, qpos, i * chunk, (i + 1) * chunk < Sk ? (i + 1) * chunk : Sk, J->block_n,
+                 J->block_n, Oc, &mc, &lc, S, P);
     if (mc == -INFINITY || lc <= 0.0) continue;
     if (M == -INFINITY) {
       M = mc; L = lc;
@@ -394,7 +404,7 @@ static void *worker(void *arg) {
 
 static int run_attention(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,
                          const uint8_t *k, const uint8_t *k_sc, const uint8_t *v, const uint8_t *v_sc,
-                         float *o, int block_n, int split_len, int dense,
+                         float *o, int block_n, int split_len, int n_parts, int dense,
                          const int32_t *heads, int nheads, int nthreads) {
   if (!p || p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0 || p->seq_q <= 0 ||
       p->seq_k <= 0 || p->head_dim <= 0 || p->head_dim % 32 || p->seq_k % 32 ||
@@ -403,6 +413,7 @@ static int run_attention(const orc_attn_params *p, const uint8_t *q, const uint8
   if (!dense && (block_n <= 0 || block_n % 32 || block_n > ORC_MAX_BLOCK_N)) return -1;
   if (p->p_rule != ORC_P_R1 && p->p_rule != ORC_P_R2) return -1;
   if (split_len < 0 || (split_len > 0 && split_len % block_n)) return -1;
+  if (n_parts < 0 || (n_parts > 0 && split_len > 0)) return -1;
   int64_t nbh = (int64_t)p->batch * p->num_q_heads;
   int64_t nkv = (int64_t)p->batch * p->num_kv_heads;
   int grp = p->num_q_heads / p->num_kv_heads;
@@ -412,7 +423,7 @@ static int run_attention(const orc_attn_params *p, const uint8_t *q, const uint8
   job_t J;
   memset(&J, 0, sizeof J);
   J.p = p; J.q = q; J.q_sc = q_sc; J.k = k; J.k_sc = k_sc; J.v = v; J.v_sc = v_sc; J.o = o;
-  J.block_n = block_n; J.split_len = split_len; J.dense = dense; J.heads = heads; J.nheads = nheads;
+  J.block_n = block_n; J.split_len = split_len; J.n_parts = n_parts; J.dense = dense; J.heads = heads; J.nheads = nheads;
   J.kd = calloc((size_t)nkv, sizeof(double *));
   J.vd = calloc((size_t)nkv, sizeof(double *));
   int64_t kvsz = (int64_t)p->seq_k * p->head_dim;
@@ -441,14 +452,15 @@ static int run_attention(const orc_attn_params *p, const uint8_t *q, const uint8
 
 int orc_attention(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,
                   const uint8_t *k, const uint8_t *k_sc, const uint8_t *v, const uint8_t *v_sc,
-                  float *o, int block_n, int split_len, const int32_t *heads, int nheads, int nthreads) {
-  return run_attention(p, q, q_sc, k, k_sc, v, v_sc, o, block_n, split_len, 0, heads, nheads, nthreads);
+                  float *o, int block_n, int split_len, int n_parts, const int32_t *heads, int nheads,
+                  int nthreads) {
+  return run_attention(p, q, q_sc, k, k_sc, v, v_sc, o, block_n, split_len, n_parts, 0, heads, nheads, nthreads);
 }
 
 int orc_attention_dense(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,
                         const uint8_t *k, const uint8_t *k_sc, const uint8_t *v, const uint8_t *v_sc,
                         float *o, const int32_t *heads, int nheads, int nthreads) {
-  return run_attention(p, q, q_sc, k, k_sc, v, v_sc, o, 32, 0, 1, heads, nheads, nthreads);
+  return run_attention(p, q, q_sc, k, k_sc, v, v_sc, o, 32, 0, 0, 1, heads, nheads, nthreads);
 }
 
 /* ------------------------------------------------------------ self-checks */

@@ -89,9 +89,11 @@ typedef struct {
 #define ORC_MAX_BLOCK_N 4096
 
 /* Streaming MX attention over key blocks of block_n keys (block j covers keys
- * [j*block_n, (j+1)*block_n)).  split_len > 0 splits the keys into independent
- * chunks of split_len keys that are merged by log-sum-exp (the split-KV decode
- * schedule); 0 = one pass.  heads: optional list of nheads flattened (b*Hq+h)
+ * [j*block_n, (j+1)*block_n)).  Split-KV: n_parts > 0 makes n_parts independent
+ * partials, partial i taking the blocks i, i + n_parts, i + 2 n_parts, ... (the
+ * interleaved decode schedule of libmxfa); else split_len > 0 splits the keys into
+ * contiguous chunks of split_len keys; partials are merged in order by log-sum-exp;
+ * both 0 = one pass.  heads: optional list of nheads flattened (b*Hq+h)
  * indices to compute (others untouched); NULL = all.  Layouts:
  *   q [B][Hq][Sq][D], q_sc [B][Hq][Sq][D/32]
  *   k [B][Hkv][Sk][D], k_sc [B][Hkv][Sk][D/32]
@@ -102,7 +104,7 @@ int orc_attention(const orc_attn_params *p,
                   const uint8_t *q, const uint8_t *q_sc,
                   const uint8_t *k, const uint8_t *k_sc,
                   const uint8_t *v, const uint8_t *v_sc,
-                  float *o, int block_n, int split_len,
+                  float *o, int block_n, int split_len, int n_parts,
                   const int32_t *heads, int nheads, int nthreads);
 
 /* Unquantized fp64 softmax attention on the dequantized operands (no P

@@ -59,7 +59,8 @@ def lib():
         L.orc_quantize_rows.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, u8p, u8p]
         L.orc_quantize_cols.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, u8p, u8p]
         L.orc_attention.argtypes = [P(AttnParams), u8p, u8p, u8p, u8p, u8p, u8p, f32p,
-                                    ctypes.c_int, ctypes.c_int, P(ctypes.c_int32), ctypes.c_int, ctypes.c_int]
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, P(ctypes.c_int32), ctypes.c_int,
+                                    ctypes.c_int]
         L.orc_attention.restype = ctypes.c_int
         L.orc_attention_dense.argtypes = [P(AttnParams), u8p, u8p, u8p, u8p, u8p, u8p, f32p,
                                           P(ctypes.c_int32), ctypes.c_int, ctypes.c_int]
@@ -194,8 +195,10 @@ def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=N
                       float(scale if scale is not None else 1.0 / np.sqrt(D)), float(softcap), v_fmt, p_rule)
 
 
-def attention(p, q, qs, k, ks, v, vs, block_n, split_len=0, heads=None, nthreads=None, out=None):
-    """Streaming MX attention oracle.  Returns fp32 O [B][Hq][Sq][D] (heads not listed are 0)."""
+def attention(p, q, qs, k, ks, v, vs, block_n, split_len=0, heads=None, nthreads=None, out=None, n_parts=0):
+    """Streaming MX attention oracle.  Returns fp32 O [B][Hq][Sq][D] (heads not listed are 0).
+    n_parts > 0: that many interleaved partials (partial i = key blocks i, i + n_parts, ...);
+    split_len > 0: contiguous chunks of split_len keys; partials merged by log-sum-exp."""
     if nthreads is None:
         nthreads = os.cpu_count() or 1
     arrs = [np.ascontiguousarray(a, dtype=np.uint8) for a in (q, qs, k, ks, v, vs)]
@@ -204,7 +207,8 @@ def attention(p, q, qs, k, ks, v, vs, block_n, split_len=0, heads=None, nthreads
     if heads is not None:
         h = np.ascontiguousarray(np.asarray(heads, dtype=np.int32))
         hp, nh = h.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(h)
-    rc = lib().orc_attention(ctypes.byref(p), *[_u8(a) for a in arrs], _f32(o), block_n, split_len, hp, nh, nthreads)
+    rc = lib().orc_attention(ctypes.byref(p), *[_u8(a) for a in arrs], _f32(o), block_n, split_len, n_parts, hp, nh,
+                                 nthreads)
     if rc != 0:
         raise ValueError("orc_attention rejected its arguments")
     return o

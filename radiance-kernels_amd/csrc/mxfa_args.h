@@ -18,8 +18,8 @@ struct FaArgs {
   int group;          // Hq / Hkv
   int hpw;            // prefill: query heads per workgroup
   int qpw;            // prefill: query positions per workgroup
-  int n_qblk;         // prefill: query blocks; decode: number of partials per query head
-  int split_len;      // decode: keys per partial (multiple of 64)
+  int n_qblk;         // prefill: query blocks; decode: interleaved partials per query head
+  int split_len;      // unused (0)
   int fuse_combine;   // decode (D <= 128): the chunks of a head merge inside the workgroup
   float c_log2;       // softmax_scale * log2(e)  (no softcap)
   float sc_u;         // softmax_scale / softcap

@@ -176,11 +176,14 @@ const char* kernel_name(const char* kind, const mxfa_attn_params* p) {
   return buf;
 }
 
-// Split-KV plan: chunks of split_len keys (a multiple of 64) so that about kDecodeWaves
-// chunk waves cover the cache -- one wave per SIMD of the 256-CU chip: one round of long
-// chunks, each wave keeping the next block's K and V in flight, few partials to merge.
-// MXFA_DECODE_WAVES overrides the target.
-constexpr int64_t kDecodeWaves = 1024;
+// Split-KV plan: the 64-key blocks of each (b, KV head) are dealt to n_parts interleaved
+// partials (partial i: blocks i, i + n_parts, ...), one wave each, about kDecodeWaves
+// partial waves per call -- two per SIMD of the 256-CU chip.  At most 4 partials are
+// rounded up to 1, 2 or 4 so that a head's partials fill whole 4-wave workgroups and merge
+// inside them.  Interleaving puts the partial waves of a head, which share a workgroup,
+// on adjacent blocks at the same time (measured on c5: 188 us vs 204 us for contiguous
+// chunks at 2048 waves).  MXFA_DECODE_WAVES overrides the target.
+constexpr int64_t kDecodeWaves = 2048;
 
 int64_t decode_wave_target() {
   if (const char* env = getenv("MXFA_DECODE_WAVES")) {
@@ -190,16 +193,14 @@ int64_t decode_wave_target() {
   return kDecodeWaves;
 }
 
-void decode_geometry(const mxfa_attn_params* p, int* split_len, int* nparts) {
-  int64_t bk = (int64_t)p->batch * p->num_kv_heads;
-  const int64_t waves = decode_wave_target();
-  int64_t target = (waves + bk - 1) / bk;
-  if (target < 1) target = 1;
-  int64_t len = (p->seq_k + target - 1) / target;
-  len = (len + 63) / 64 * 64;
-  if (len < 64) len = 64;
-  *split_len = (int)len;
-  *nparts = (int)((p->seq_k + len - 1) / len);
+int decode_parts(const mxfa_attn_params* p) {
+  const int64_t bk = (int64_t)p->batch * p->num_kv_heads;
+  const int64_t blocks = (p->seq_k + 63) / 64;
+  int64_t n = (decode_wave_target() + bk - 1) / bk;
+  if (n == 3) n = 4;
+  if (n > blocks) n = blocks;
+  if (n < 1) n = 1;
+  return (int)n;
 }
 
 }  // namespace
@@ -400,11 +401,10 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   return launch(dm, kernel_name("prefill", p), grid, dim3(256), args, stream);
 }
 
-mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* split_len, size_t* workspace_bytes) {
+mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* n_parts, size_t* workspace_bytes) {
   if (mxfa_status st = check_params(p, true)) return st;
-  int sl, np;
-  decode_geometry(p, &sl, &np);
-  if (split_len) *split_len = sl;
+  const int np = decode_parts(p);
+  if (n_parts) *n_parts = np;
   if (workspace_bytes)
     *workspace_bytes = (size_t)p->batch * p->num_q_heads * np * (p->head_dim + 2) * sizeof(float) + 256;
   return MXFA_OK;
@@ -425,9 +425,7 @@ mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
   FaArgs a = make_args(p, q, q_sc, k_cache, k_sc, v_cache, v_sc, o);
-  int split_len, nparts;
-  decode_geometry(p, &split_len, &nparts);
-  a.split_len = split_len;
+  const int nparts = decode_parts(p);
   a.n_qblk = nparts;
   int64_t nbh = (int64_t)p->batch * p->num_q_heads;
   a.part_o = reinterpret_cast<float*>(workspace);
@@ -438,7 +436,7 @@ mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8
   const int64_t items = (int64_t)p->batch * p->num_kv_heads * nparts;
   dim3 grid = p->head_dim == 256 ? dim3((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads))
                                  : dim3((unsigned)((items + nw - 1) / nw));
-  // When every head's chunks fit in one workgroup (nparts divides its 4 waves) and the
+  // When every head's partials fit in one workgroup (nparts divides its 4 waves) and the
   // valid columns' partials fit the waves' V slots (group <= 16), the kernel merges them
   // itself (same formula and order as mxfa_decode_combine) and no combine launch follows.
   // MXFA_DECODE_COMBINE=kernel selects the combine kernel always (the two paths give

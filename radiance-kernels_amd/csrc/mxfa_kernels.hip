@@ -889,15 +889,15 @@ MXFA_PREFILL(128, true, P_R2, mxfa_prefill_d128_softcap_r2)
 MXFA_PREFILL(256, true, P_R2, mxfa_prefill_d256_softcap_r2)
 
 // ---------------------------------------------------------------------------
-// Decode (q_len = 1, split-KV).  The keys of each (b, KV head) are cut into
-// nparts chunks of split_len keys; wave w of workgroup x processes chunk
-// part = NW*x + w (NW = 4, or 2 for D = 256) as an independent streaming pass and writes its partial
-// (m, l, O); mxfa_decode_combine merges the partials in part order.  The
-// group's query heads are the wave's query columns (column c = head kvh*group + c).
+// Decode (q_len = 1, split-KV).  The 64-key blocks of each (b, KV head) are dealt to
+// nparts interleaved partials (partial i: blocks i, i + nparts, ...); one wave runs each
+// partial as an independent streaming pass and produces its (m, l, O); the partials are
+// merged in part order (inside the workgroup, or by mxfa_decode_combine).  The group's
+// query heads are the wave's query columns (column c = head kvh*group + c).
 // ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
-// Decode, D <= 128.  One wave per chunk of split_len keys of one (b, KV head); its 32
-// score columns are the group's query heads (columns >= group are padding, masked).
+// Decode, D <= 128.  One wave per partial of one (b, KV head); its 32 score columns are
+// the group's query heads (columns >= group are padding).
 // K goes straight from global memory to registers in the split-d mapping and is
 // dequantized to bf16 right before each score MFMA; only V (transposed by the
 // ds_read_b64_tr_b8 reads of the PV step) passes through the wave's LDS slot.  Small
@@ -942,19 +942,20 @@ __device__ void decode_split_impl(const FaArgs& a) {
   const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.v, (int64_t)bk * a.Sk * D, (int64_t)a.Sk * D);
   const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(a.vs, (int64_t)bk * (a.Sk / 32) * D, (int64_t)(a.Sk / 32) * D);
 
-  const int kbeg = part * a.split_len;
-  const int kend = min(kbeg + a.split_len, a.Sk);
   int klo, khi;
   key_limits(a, qpos, qvalid, klo, khi);
-  khi = min(khi, kend - 1);                          // the rest of the tile belongs to other chunks
-  // The visible range of the (single) query position, uniform over the wave: blocks
-  // outside it contribute nothing (P = 0, the max unchanged) and are not visited; blocks
-  // inside it need no mask.  Padding columns (r >= group, Q = 0) are not masked: their
-  // scores are 0, their state stays finite and is never written.
+  // Partial `part` of n_qblk takes the key blocks part, part + n_qblk, ... (interleaved:
+  // the partial waves of a head, which share a workgroup, read adjacent blocks at the
+  // same time).  The visible range of the (single) query position is uniform over the
+  // wave: blocks outside it contribute nothing (P = 0, the max unchanged) and are not
+  // visited; blocks inside it need no mask.  Padding columns (r >= group, Q = 0) are not
+  // masked: their scores are 0, their state stays finite and is never written.
   int klo_u, khi_u;
   key_limits(a, qpos, true, klo_u, khi_u);
-  khi_u = min(khi_u, kend - 1);
-  const int kfirst = max(kbeg, klo_u & ~(BN - 1)), klast = active ? min(kend, khi_u + 1) : kfirst;
+  const int kstride = a.n_qblk * BN;
+  const int blo = klo_u / BN;                         // first visible block
+  const int bfirst = blo <= part ? part : part + (blo - part + a.n_qblk - 1) / a.n_qblk * a.n_qblk;
+  const int kfirst = bfirst * BN, klast = active ? khi_u + 1 : kfirst;
 
   WaveState<D> st;
 #pragma unroll
@@ -998,7 +999,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
   // LDS, and both stay in flight through the softmax and PV of block j
   load_k(kfirst, kfirst < klast);
   load_v(kfirst, kfirst < klast);
-  for (int key0 = kfirst; key0 < klast; key0 += BN) {
+  for (int key0 = kfirst; key0 < klast; key0 += kstride) {
     // scores from registers: K dequantized to bf16 just before each MFMA
     v16f sc[NT];
 #pragma unroll
@@ -1012,7 +1013,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
         sc[t] = mfma_bf16(ka, qb[kk], sc[t]);
       }
     }
-    load_k(key0 + BN, key0 + BN < klast);
+    load_k(key0 + kstride, key0 + kstride < klast);
 #pragma unroll
     for (int i = 0; i < PERW; i++) {
       const int c = lane + 64 * i;
@@ -1024,7 +1025,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
       *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = zv;
     }
     if (lane < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * lane]) = vsr;
-    load_v(key0 + BN, key0 + BN < klast);
+    load_v(key0 + kstride, key0 + kstride < klast);
     // LDS operations of one wave complete in order: the V tile written above is in place
     // for the transposed reads, and the next block's writes follow this block's reads
     const bool mask = key0 < klo_u || key0 + BN - 1 > khi_u;
@@ -1141,11 +1142,10 @@ __device__ void decode_impl(const FaArgs& a) {
   const uint8_t* vb = a.v + (int64_t)bk * a.Sk * D;
   const uint8_t* vsb = a.vs + (int64_t)bk * (a.Sk / 32) * D;
 
-  const int kbeg = part * a.split_len;
-  const int kend = min(kbeg + a.split_len, a.Sk);
+  // partial `part` of n_qblk takes the key blocks part, part + n_qblk, ...
+  const int kend = a.Sk;
   int klo, khi;
   key_limits(a, qpos, qvalid, klo, khi);
-  khi = min(khi, kend - 1);                          // the rest of the tile belongs to other chunks
 
   WaveState<D> st;
 #pragma unroll
@@ -1158,7 +1158,7 @@ __device__ void decode_impl(const FaArgs& a) {
   constexpr int PERW = BN * CPR / 64;
   constexpr int KP = Lds<D>::KP;
   constexpr int KPB = Lds<D>::KPB;
-  for (int key0 = kbeg; key0 < kend; key0 += BN) {
+  for (int key0 = part * BN; key0 < kend; key0 += a.n_qblk * BN) {
 #pragma unroll
     for (int i = 0; i < PERW; i++) {
       int c = lane + 64 * i;

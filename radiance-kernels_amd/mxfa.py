@@ -218,10 +218,12 @@ def prefill(p, q, qs, k, ks, v, vs, out=None, stream=None):
 
 
 def decode_plan(p):
-    sl = ctypes.c_int32(0)
+    """(n_parts, workspace bytes): the decode's interleaved partials per head (partial i
+    takes key blocks i, i + n_parts, ...) and the workspace mxfa.decode needs."""
+    n = ctypes.c_int32(0)
     ws = ctypes.c_size_t(0)
-    _check(lib().mxfa_decode_plan(ctypes.byref(p), ctypes.byref(sl), ctypes.byref(ws)))
-    return sl.value, ws.value
+    _check(lib().mxfa_decode_plan(ctypes.byref(p), ctypes.byref(n), ctypes.byref(ws)))
+    return n.value, ws.value
 
 
 def decode(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):

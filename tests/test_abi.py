@@ -84,10 +84,14 @@ def test_null_and_misaligned_pointers_rejected():
 def test_decode_validation_and_plan():
     L = mxfa.lib()
     p = mxfa.make_params(64, 32, 8, 1, 8192, 128, causal=True, q_pos0=8191)
-    sl, ws = mxfa.decode_plan(p)
-    assert sl % 64 == 0 and sl >= 64
-    nparts = -(-8192 // sl)
+    nparts, ws = mxfa.decode_plan(p)
+    assert nparts == 4                       # 2048 partial waves over 512 (b, KV head) pairs
     assert ws >= 64 * 32 * nparts * (128 + 2) * 4
+    # small problems: at most one partial per 64-key block; 3 rounds up to 4
+    assert mxfa.decode_plan(mxfa.make_params(1, 8, 8, 1, 128, 64, causal=True, q_pos0=127))[0] == 2
+    assert mxfa.decode_plan(mxfa.make_params(1, 8, 1, 1, 64 * 40, 64, causal=True, q_pos0=2559))[0] == 40
+    assert mxfa.decode_plan(mxfa.make_params(8, 32, 8, 1, 4096, 128, causal=True, q_pos0=4095))[0] == 32
+    assert mxfa.decode_plan(mxfa.make_params(96, 32, 8, 1, 4096, 128, causal=True, q_pos0=4095))[0] == 4
     p2 = mxfa.make_params(1, 1, 1, 2, 64, 64)
     sl_ = ctypes.c_int32(0)
     ws_ = ctypes.c_size_t(0)

@@ -113,20 +113,20 @@ def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=
     fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L, D, seed, v_fmt=v_fmt)
     p = mxfa.make_params(B, Hq, Hkv, 1, L, D, causal=True, q_pos0=L - 1, softcap=softcap, v_fmt=v_fmt,
                          p_rule=p_rule)
-    split_len, _ = mxfa.decode_plan(p)
+    n_parts, _ = mxfa.decode_plan(p)
     out = torch.full((B, Hq, 1, D), float("nan"), dtype=torch.float32, device=DEV)
     mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
     torch.cuda.synchronize()
     o = np_(out)
     assert np.all(np.isfinite(o))
     want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
-                       block_n=mxfa.DEFAULT_BLOCK_N, split_len=split_len, heads=heads)
+                       block_n=mxfa.DEFAULT_BLOCK_N, n_parts=n_parts, heads=heads)
     if heads is not None:
         idx = np.array(heads)
         o = o.reshape(B * Hq, D)[idx]
         want = want.reshape(B * Hq, D)[idx]
     rel, mab = errors(o, want)
-    print(f"   split_len {split_len} rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+    print(f"   n_parts {n_parts} rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
     assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
     return p, dev, out
 
@@ -149,16 +149,17 @@ def test_decode_config5_sampled():
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,L,D,waves,window,softcap", [
-    (4, 32, 8, 1024, 128, 32, 0, 0.0),        # 1 chunk per head
-    (4, 32, 8, 1024, 128, 64, 0, 0.0),        # 2 chunks
-    (4, 32, 8, 1024, 128, 128, 300, 0.0),     # 4 chunks, window (leading chunks skip blocks)
-    (3, 8, 2, 480, 64, 24, 0, 30.0),          # 4 ragged chunks, softcap, D = 64
+    (4, 32, 8, 1024, 128, 32, 0, 0.0),        # 1 partial per head
+    (4, 32, 8, 1024, 128, 64, 0, 0.0),        # 2 partials
+    (4, 32, 8, 1024, 128, 128, 300, 0.0),     # 4 partials, window (partials start past block 0)
+    (3, 8, 2, 480, 64, 18, 0, 30.0),          # 3 -> 4 partials, ragged last block, softcap, D = 64
     (2, 64, 4, 1056, 128, 16, 0, 0.0),        # group 16, ragged last block
-    (4, 32, 8, 1024, 128, 96, 0, 0.0),        # 3 chunks: not fused, both runs use the kernel
+    (4, 32, 8, 1024, 128, 256, 0, 0.0),       # 8 partials: not fused, both runs use the kernel
 ])
 def test_decode_fused_merge_matches_combine_kernel(monkeypatch, B, Hq, Hkv, L, D, waves, window, softcap):
-    """The in-workgroup merge of the chunk partials (one launch) and mxfa_decode_combine
-    (two launches) give bit-identical O: same partials, same formula, same chunk order."""
+    """The in-workgroup merge of the interleaved partials (one launch) and
+    mxfa_decode_combine (two launches) give bit-identical O: same partials, same formula,
+    same order."""
     print(f"decode fused-vs-kernel B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} waves {waves}", flush=True)
     monkeypatch.setenv("MXFA_DECODE_WAVES", str(waves))
     fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L, D, seed=40 + waves)
@@ -170,9 +171,9 @@ def test_decode_fused_merge_matches_combine_kernel(monkeypatch, B, Hq, Hkv, L, D
     torch.cuda.synchronize()
     assert torch.isfinite(fused).all()
     assert torch.equal(fused, combined)
-    split_len, _ = mxfa.decode_plan(p)
+    n_parts, _ = mxfa.decode_plan(p)
     want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
-                       block_n=mxfa.DEFAULT_BLOCK_N, split_len=split_len)
+                       block_n=mxfa.DEFAULT_BLOCK_N, n_parts=n_parts)
     rel, mab = errors(np_(fused), want)
     assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
 

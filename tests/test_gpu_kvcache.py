@@ -78,9 +78,9 @@ def test_decode_over_appended_cache():
     v, vs = cache.v[:, :, :sk].contiguous(), cache.vs[:, :, :sk // 32].contiguous()
     o = mxfa.decode(p, q, qs, k, ks, v, vs)
     torch.cuda.synchronize()
-    split_len, _ = mxfa.decode_plan(p)
+    n_parts, _ = mxfa.decode_plan(p)
     want = O.attention(oracle_params(p), np_(q), np_(qs), np_(k), np_(ks), np_(v), np_(vs),
-                       block_n=mxfa.DEFAULT_BLOCK_N, split_len=split_len)
+                       block_n=mxfa.DEFAULT_BLOCK_N, n_parts=n_parts)
     rel, mab = errors(np_(o), want)
     print(f"   decode over appended cache: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
     assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL

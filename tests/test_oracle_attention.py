@@ -85,6 +85,13 @@ def test_blocking_exact_when_max_in_first_key():
     ref = O.attention(p, q, qs, k, ks, v, vs, block_n=256)
     o = O.attention(p, q, qs, k, ks, v, vs, block_n=64, split_len=128)
     np.testing.assert_allclose(o, ref, rtol=1e-9, atol=1e-12)
+    # interleaved partials (partial i = blocks i, i + n, ...): with copies of the dominating
+    # key at the start of blocks 0 and 1, both partials of n = 2 see the global max first
+    K[:, :, 64] = K[:, :, 0]
+    q, qs, k, ks, v, vs = quantize_qkv(Q, K, V)
+    ref = O.attention(p, q, qs, k, ks, v, vs, block_n=256)
+    o = O.attention(p, q, qs, k, ks, v, vs, block_n=64, n_parts=2)
+    np.testing.assert_allclose(o, ref, rtol=1e-9, atol=1e-12)
 
 
 def test_streaming_close_to_dense_and_fp32():
@@ -175,6 +182,30 @@ def test_split_kv_close_to_single_pass():
     b = O.attention(p, *ops, block_n=64, split_len=256)
     d = O.attention_dense(p, *ops)
     assert rel_l2(b, a) < 0.06 and rel_l2(b, d) < 0.06
+
+
+def test_interleaved_partials_schedule():
+    """n_parts = 1 is the single pass bit for bit; n_parts = number of blocks makes every
+    block its own partial, which equals contiguous chunks of one block (split_len =
+    block_n) bit for bit; other n_parts differ from the single pass by about the MX
+    quantization error.  A schedule that merged partials out of order or took the
+    blocks contiguously would fail the identities below."""
+    B, Hq, Hkv, Sk, D = 2, 8, 2, 512, 64
+    Q, K, V = normal_inputs(B, Hq, Hkv, 1, Sk, D, seed=21)
+    ops = quantize_qkv(Q, K, V)
+    p = O.make_params(B, Hq, Hkv, 1, Sk, D, causal=True, q_pos0=Sk - 1)
+    one = O.attention(p, *ops, block_n=64)
+    np.testing.assert_array_equal(O.attention(p, *ops, block_n=64, n_parts=1), one)
+    np.testing.assert_array_equal(O.attention(p, *ops, block_n=64, n_parts=8),
+                                  O.attention(p, *ops, block_n=64, split_len=64))
+    four = O.attention(p, *ops, block_n=64, n_parts=4)
+    assert 0 < rel_l2(four, one) < 0.06
+    assert not np.array_equal(four, O.attention(p, *ops, block_n=64, split_len=128))
+    # partial i of n = 2 over a cache whose odd blocks are all masked (window) equals one
+    # pass over the even blocks: here the window keeps only the last block (7, odd), so
+    # n = 2 leaves partial 0 empty and equals the single pass
+    pw = O.make_params(B, Hq, Hkv, 1, Sk, D, causal=True, q_pos0=Sk - 1, window=64)
+    np.testing.assert_array_equal(O.attention(pw, *ops, block_n=64, n_parts=2), O.attention(pw, *ops, block_n=64))
 
 
 def test_e3m2_v_operand():
