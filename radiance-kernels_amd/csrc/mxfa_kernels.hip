@@ -1271,54 +1271,64 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_decode_combine(FaArgs a) 
 // parameter (widened to E4M3 on the way into LDS, exact), the scale staging is spread over
 // all threads without branches, and the last step is peeled.
 // ---------------------------------------------------------------------------
+#ifndef MXFA_GEMM_TK
+#define MXFA_GEMM_TK 128
+#endif
 namespace gemm {
-constexpr int TM = 256, TN = 256, TK = 64;
-constexpr int AP = TK + 16;                // A row pitch in LDS (bytes)
+constexpr int TM = 256, TN = 256, TK = MXFA_GEMM_TK;
+constexpr int AP = TK + 16;                // A row pitch in LDS (bytes; conflict-free b128 rows)
 constexpr int BP = TN + 16;                // B row pitch (bytes)
 constexpr int A_BYTES = TM * AP, B_BYTES = TK * BP;
-constexpr int S_BYTES = 2 * TM + 2 * TN;   // SA [2][TM] then SB [2][TN]
+constexpr int KB = TK / 32;                // scale blocks per step
+constexpr int S_BYTES = KB * (TM + TN);    // SA [KB][TM] then SB [KB][TN]
 constexpr int NT = 512;                    // threads per workgroup
-static_assert(TM == TN && S_BYTES == 2 * NT, "one 2-byte scale pair per thread");
+constexpr int CH = TK / 32;                // 16-byte chunks of A (and of B) per thread per step
+constexpr int SPT = S_BYTES / NT;          // scale bytes per thread per step
+static_assert(TM == TN && (TK == 64 || TK == 128), "tile shape");
 }  // namespace gemm
 
 struct GemmStage {
-  v4i a[2];                                // A: 256 rows x 64 B = 1024 chunks, 2 per thread
-  v4i b[2];                                // B: 64 rows x 256 B = 1024 chunks, 2 per thread
-  uint32_t s;                              // two scale codes (threads 0-255 SA, 256-511 SB)
+  v4i a[gemm::CH];                         // A: 256 rows x TK B
+  v4i b[gemm::CH];                         // B: TK rows x 256 B
+  uint32_t s;                              // SPT scale codes (threads 0-255 SA, 256-511 SB)
 };
 
 struct GemmRes {
   __amdgpu_buffer_rsrc_t a;                // rows m0 .. M of A
-  int64_t soff;                            // this thread's scale row base (B offset of k0 = 0)
   const uint8_t* sbase;                    // SA or SB (uniform per wave)
   int sdim;                                // M or N
-  uint32_t svoff;                          // offset of the thread's pair within a k-step
+  uint32_t svoff;                          // offset of the thread's scale codes within a k-step
 };
 
-// Loads of a step at k0 >= K read nothing and return zeros (E8M0 code 0 = 2^-127 scales,
-// so that step adds exact zeros).
+// Everything at k >= K reads as zero (E8M0 code 0 = 2^-127 scales, so such a step, or the
+// part of one past K when K % TK == 64, adds exact zeros): A chunks past K get an offset
+// outside the resource, the B and scale resources end at K.
 __device__ __forceinline__ void gemm_load(GemmStage& r, const GemmArgs& g, const GemmRes& res, int n0, int k0, int tid) {
   using namespace gemm;
-  const bool on = k0 < g.K;
-  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, (int64_t)k0 * g.N, on ? (int64_t)TK * g.N : 0);
+  const int krem = max(0, min(TK, g.K - k0));                   // rows of this step below K
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, (int64_t)k0 * g.N, (int64_t)krem * g.N);
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < CH; i++) {
     const int c = tid + NT * i;
-    const int row = c >> 2, col = (c & 3) * 16;                  // A chunk: row, 16-byte column
-    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, on ? (uint32_t)(row * g.K + k0 + col) : 0x80000000u, 0, 0);
+    const int row = c / (TK / 16), col = (c % (TK / 16)) * 16;  // A chunk: row, 16-byte column
+    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, col < krem ? (uint32_t)(row * g.K + k0 + col) : 0x80000000u,
+                                                   0, 0);
     const int kr = c >> 4, bc = (c & 15) * 16;                   // B chunk: k row, column
     const uint32_t bo = n0 + bc < g.N ? (uint32_t)(kr * g.N + n0 + bc) : 0x80000000u;
     r.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, bo, 0, 0);
   }
-  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, on ? 2 * (int64_t)res.sdim : 0);
-  r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, res.svoff, 0, 0);
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, (int64_t)(krem / 32) * res.sdim);
+  if constexpr (SPT == 4)
+    r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, res.svoff, 0, 0);
+  else
+    r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, res.svoff, 0, 0);
 }
 
 template <int AE3, int BE3>
 __device__ __forceinline__ void gemm_store(const GemmStage& r, uint8_t* sA, uint8_t* sB, uint8_t* sS, int tid) {
   using namespace gemm;
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < CH; i++) {
     const int c = tid + NT * i;
     v4i va = r.a[i], vb = r.b[i];
     if (AE3) {
@@ -1329,10 +1339,13 @@ __device__ __forceinline__ void gemm_store(const GemmStage& r, uint8_t* sA, uint
 #pragma unroll
       for (int w = 0; w < 4; w++) vb[w] = (int)e3m2x4_to_e4m3x4((uint32_t)vb[w]);
     }
-    *reinterpret_cast<v4i*>(sA + (c >> 2) * AP + (c & 3) * 16) = va;
+    *reinterpret_cast<v4i*>(sA + (c / (TK / 16)) * AP + (c % (TK / 16)) * 16) = va;
     *reinterpret_cast<v4i*>(sB + (c >> 4) * BP + (c & 15) * 16) = vb;
   }
-  *reinterpret_cast<uint16_t*>(sS + 2 * tid) = (uint16_t)r.s;
+  if constexpr (SPT == 4)
+    *reinterpret_cast<uint32_t*>(sS + 4 * tid) = r.s;
+  else
+    *reinterpret_cast<uint16_t*>(sS + 2 * tid) = (uint16_t)r.s;
 }
 
 // One k-step of the wave's 4 x 2 MFMA tiles from one LDS stage.
@@ -1342,29 +1355,32 @@ __device__ __forceinline__ void gemm_mma(v16f (&acc)[4][2], const uint8_t* sA, c
   const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
   // operands: A row tile i (rows 128 wr + 32 i + r, k = 16 h .. and 32 + 16 h ..), B
   // column tile j (column 64 wc + 32 j + 16 (g16 & 1) + l16, k rows via transposed reads)
-  v8i bo[2];
-  int bsc[2];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int ncol = 64 * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
+  for (int kh = 0; kh < TK / 64; kh++) {                // 64-k halves of the step
+    v8i bo[2];
+    int bsc[2];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int krow = 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
-      v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB + krow * BP + ncol));
-      bo[j][2 * q] = t[0];
-      bo[j][2 * q + 1] = t[1];
+    for (int j = 0; j < 2; j++) {
+      const int ncol = 64 * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int krow = 64 * kh + 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
+        v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB + krow * BP + ncol));
+        bo[j][2 * q] = t[0];
+        bo[j][2 * q + 1] = t[1];
+      }
+      bsc[j] = sS[KB * TM + (2 * kh + h) * TN + 64 * wc + 32 * j + r];
     }
-    bsc[j] = sS[2 * TM + h * TN + 64 * wc + 32 * j + r];
-  }
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int row = 128 * wr + 32 * i + r;
-    const v4i lo = *reinterpret_cast<const v4i*>(sA + row * AP + 16 * h);
-    const v4i hi = *reinterpret_cast<const v4i*>(sA + row * AP + 32 + 16 * h);
-    const v8i ao = cat44(lo, hi);
-    const int asc = sS[h * TM + row];
+    for (int i = 0; i < 4; i++) {
+      const int row = 128 * wr + 32 * i + r;
+      const v4i lo = *reinterpret_cast<const v4i*>(sA + row * AP + 64 * kh + 16 * h);
+      const v4i hi = *reinterpret_cast<const v4i*>(sA + row * AP + 64 * kh + 32 + 16 * h);
+      const v8i ao = cat44(lo, hi);
+      const int asc = sS[(2 * kh + h) * TM + row];
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
+      for (int j = 0; j < 2; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
+    }
   }
 }
 
@@ -1393,12 +1409,13 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
   GemmRes res;
   res.a = buf_rsrc(g.a, (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
   {
-    // thread t stages scale codes [k0/32 + kb][c0 + 2 cp ..+2] of SA (t < 256) or SB
+    // thread t stages scale codes [k0/32 + kb][c0 + SPT cp .. + SPT] of SA (t < 256) or SB;
+    // its LDS bytes are SPT t ..
     const bool is_a = wave < 4;
-    const int t = tid & 255, kb = t >> 7, cp = t & 127;
+    const int t = tid & 255, kb = t / (256 / SPT), cp = t % (256 / SPT);
     res.sbase = is_a ? g.sa : g.sb;
     res.sdim = is_a ? g.M : g.N;
-    const int c = (is_a ? m0 : n0) + 2 * cp;
+    const int c = (is_a ? m0 : n0) + SPT * cp;
     res.svoff = c < res.sdim ? (uint32_t)(kb * res.sdim + c) : 0x80000000u;
   }
 
@@ -1408,10 +1425,29 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = (v16f){};
 
+  const int nk = (g.K + TK - 1) / TK;
+  if constexpr (TK == 128) {
+    // One register stage: step k + 1 is loaded while step k is multiplied, then stored
+    // into the other LDS stage.
+    GemmStage st;
+    gemm_load(st, g, res, n0, 0, tid);
+    gemm_store<AE3, BE3>(st, sA[0], sB[0], sS[0], tid);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+      const int buf = kt & 1;
+      // loads go out first and the MFMAs before the wait of the stores (the scheduler
+      // otherwise sinks the loads between the MFMAs to save registers)
+      gemm_load(st, g, res, n0, (kt + 1) * TK, tid);
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_mma(acc, sA[buf], sB[buf], sS[buf], wr, wc, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_store<AE3, BE3>(st, sA[buf ^ 1], sB[buf ^ 1], sS[buf ^ 1], tid);
+      __syncthreads();
+    }
+  } else {
   // Two register stages: step k + 2 is loaded while step k is multiplied and step k + 1
   // (loaded one step earlier) goes into the other LDS stage.  The loop runs steps in
-  // pairs; for odd K / 64 the last step multiplies zeros.
-  const int nk = g.K / TK;
+  // pairs; for an odd step count the last step multiplies zeros.
   GemmStage s0, s1;
   gemm_load(s0, g, res, n0, 0, tid);
   gemm_load(s1, g, res, n0, TK, tid);
@@ -1432,6 +1468,7 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
     __builtin_amdgcn_sched_barrier(0);
     gemm_store<AE3, BE3>(s0, sA[0], sB[0], sS[0], tid);
     __syncthreads();
+  }
   }
 
   // C tile: lane l, register v of tile (i, j) -> row 128 wr + 32 i + 8 (v / 4) + 4 h + v % 4,
