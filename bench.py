@@ -150,9 +150,15 @@ def bench_gemm(torch, mxfa, args):
     c = torch.empty((M, N), dtype=torch.float32, device=dev)
     ms = time_calls(torch, lambda: mxfa.gemm(xq, xs, wq, ws, out=c), args.steps, args.warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    del c
+    c16 = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms16 = time_calls(torch, lambda: mxfa.gemm(xq, xs, wq, ws, out=c16, c_fmt=mxfa.C_BF16), args.steps, args.warmup)
+    tf16 = 2.0 * M * N * K / (ms16 * 1e-3) / 1e12
     return {"workload": f"QKV projection of configs[2]: M={M} N={N} K={K}, E4M3 x E4M3 -> fp32",
             "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_call": round(ms, 4),
-            "frac_mxfp8_peak": round(tflops / MXFP8_PEAK_TFLOPS, 4)}
+            "frac_mxfp8_peak": round(tflops / MXFP8_PEAK_TFLOPS, 4),
+            "bf16_out": {"value": round(tf16, 1), "unit": "TFLOP/s", "ms_per_call": round(ms16, 4),
+                         "frac_mxfp8_peak": round(tf16 / MXFP8_PEAK_TFLOPS, 4)}}
 
 
 def cpu_baseline(mxfa, p, ops_host, threads):

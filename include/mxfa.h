@@ -172,21 +172,29 @@ mxfa_status mxfa_softmax_requant(const float *s, const float *row_max, float c, 
 
 /* Shape and element formats of mxfa_gemm (the reference's MATMUL_M/N/K defines,
  * kernels/gemm_mxgemmini/gen_mxgemm_data.py:105-107). */
+typedef enum {
+  MXFA_C_F32 = 0,                           /* fp32 C                                           */
+  MXFA_C_BF16 = 1                           /* bf16 C (round to nearest even of the fp32 sum;   */
+                                            /* the reference's C_out_bf16 format)               */
+} mxfa_c_fmt;
+
 typedef struct {
   int64_t m, n, k;                          /* m % 16 == 0, n % 16 == 0, k % 64 == 0 (> 0)     */
   int32_t a_fmt, b_fmt;                     /* mxfa_fmt of the A and B element codes            */
+  int32_t c_fmt;                            /* mxfa_c_fmt of the output                         */
 } mxfa_gemm_params;
 
 /* C = A x B with MX operands in the reference MX GEMM's layouts (A_in [M][K], B_in [K][N],
  * A_scales_row [K/32][M], B_scales_col [K/32][N]; kernels/gemm_mxgemmini/gen_mxgemm_data.py:
  * 118-126, lib/golden/mx_golden.cpp:23-30): C[m][n] = sum over 32-groups g of K of
- * 2^(a_sc[g][m] + b_sc[g][n] - 254) * sum_{k in g} A[m][k] B[k][n], fp32 output c [M][N].
+ * 2^(a_sc[g][m] + b_sc[g][n] - 254) * sum_{k in g} A[m][k] B[k][n], output c [M][N] in fp32
+ * or bf16 (c_fmt; the reference's golden writes bf16, kernels/gemm_mxgemmini_ws/kernel.cpp:17).
  * Replaces the Gemmini MX GEMM driver's tile loop (lib/mxgemm/mxgemm_lib.hpp:11-250) with the
  * scaled MXFP8 MFMA (fp32 accumulation, not Gemmini's narrow accumulators).  The reference's
  * requant output (C_out + C_scales_row, rule R1) is mxfa_quantize_rows applied to c (scales
  * then [M][N/32], the transpose of C_scales_row). */
 mxfa_status mxfa_gemm(const mxfa_gemm_params *p, const uint8_t *a, const uint8_t *a_sc,
-                      const uint8_t *b, const uint8_t *b_sc, float *c, void *stream);
+                      const uint8_t *b, const uint8_t *b_sc, void *c, void *stream);
 
 /* Synthetic inputs: x[i] ~ N(0,1) (counter-based hash + Box-Muller), each element
  * multiplied by outlier_mul with probability outlier_p.  Replaces make_inputs /

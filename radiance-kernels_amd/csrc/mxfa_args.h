@@ -33,9 +33,10 @@ struct GemmArgs {
   const uint8_t* sa;
   const uint8_t* b;
   const uint8_t* sb;
-  float* c;
+  uint8_t* c;         // fp32 or bf16 C [M][N]
   int M, N, K;
   int b_e3m2;         // B element codes are E3M2 (widened to E4M3 on the way to LDS)
   int a_e3m2;         // A element codes are E3M2
-  int tiles_n;        // number of 128-column tiles
+  int tiles_n;        // number of 256-column tiles
+  int c_bf16;         // C is written as bf16 (round to nearest even)
 };

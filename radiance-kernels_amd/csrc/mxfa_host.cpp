@@ -343,7 +343,7 @@ mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, 
 }
 
 mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t* a_sc, const uint8_t* b,
-                      const uint8_t* b_sc, float* c, void* stream) {
+                      const uint8_t* b_sc, void* c, void* stream) {
   if (!p) return fail(MXFA_ERR_INVALID_ARG, "params is NULL");
   if (p->m < 1 || p->n < 1 || p->k < 1) return fail(MXFA_ERR_INVALID_ARG, "m, n and k must be >= 1");
   if (p->k % 32) return fail(MXFA_ERR_INVALID_ARG, "k must be a multiple of 32 (scale blocks)");
@@ -351,6 +351,7 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
     return fail(MXFA_ERR_UNSUPPORTED, "mxfa_gemm needs k % 64 == 0, m % 16 == 0 and n % 16 == 0");
   if (p->a_fmt != MXFA_FMT_E4M3 && p->a_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad a_fmt");
   if (p->b_fmt != MXFA_FMT_E4M3 && p->b_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad b_fmt");
+  if (p->c_fmt != MXFA_C_F32 && p->c_fmt != MXFA_C_BF16) return fail(MXFA_ERR_INVALID_ARG, "bad c_fmt");
   const int64_t lim = (int64_t)1 << 31;
   if (p->m * p->k >= lim || p->k * p->n >= lim)
     return fail(MXFA_ERR_UNSUPPORTED, "mxfa_gemm operands are limited to 2^31 elements");
@@ -362,7 +363,8 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
   if (mxfa_status st = module_for_current(&dm)) return st;
   GemmArgs g;
   std::memset(&g, 0, sizeof g);
-  g.a = a; g.sa = a_sc; g.b = b; g.sb = b_sc; g.c = c;
+  g.a = a; g.sa = a_sc; g.b = b; g.sb = b_sc; g.c = static_cast<uint8_t*>(c);
+  g.c_bf16 = p->c_fmt == MXFA_C_BF16;
   g.M = (int)p->m; g.N = (int)p->n; g.K = (int)p->k;
   g.a_e3m2 = p->a_fmt == MXFA_FMT_E3M2;
   g.b_e3m2 = p->b_fmt == MXFA_FMT_E3M2;

@@ -1473,21 +1473,25 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
 
   // C tile: lane l, register v of tile (i, j) -> row 128 wr + 32 i + 8 (v / 4) + 4 h + v % 4,
   // column 64 wc + 32 j + r.  Rows >= M fall outside the tile's resource; columns >= N get
-  // an offset outside every resource.
+  // an offset outside every resource.  ES = bytes per C element (4 fp32, 2 bf16).
   const int r = lane & 31, h = lane >> 5;
   const int rows = min(TM, g.M - m0);
+  const int ES = g.c_bf16 ? 2 : 4;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(g.c + (int64_t)m0 * g.N), 0, (int)(uint32_t)((int64_t)rows * g.N * 4), 0x00020000);
+      (void*)(g.c + (int64_t)m0 * g.N * ES), 0, (int)(uint32_t)((int64_t)rows * g.N * ES), 0x00020000);
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int n = n0 + 64 * wc + 32 * j + r;
-    const uint32_t cb = n < g.N ? (uint32_t)((128 * wr + 4 * h) * g.N + n) * 4u : 0xfffffff0u;
+    const uint32_t cb = n < g.N ? (uint32_t)((128 * wr + 4 * h) * g.N + n) * (uint32_t)ES : 0xfffffff0u;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const uint32_t off = n < g.N ? cb + (uint32_t)((32 * i + 8 * (v >> 2) + (v & 3)) * g.N) * 4u : cb;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), rc, off, 0, 0);
+        const uint32_t off = n < g.N ? cb + (uint32_t)((32 * i + 8 * (v >> 2) + (v & 3)) * g.N) * (uint32_t)ES : cb;
+        if (g.c_bf16)
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)acc[i][j][v]), rc, off, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), rc, off, 0, 0);
       }
   }
 }

@@ -64,9 +64,12 @@ class KvParams(ctypes.Structure):
                 ("max_len", ctypes.c_int32), ("v_fmt", ctypes.c_int32)]
 
 
+C_F32, C_BF16 = 0, 1                    # mxfa_c_fmt
+
+
 class GemmParams(ctypes.Structure):
     _fields_ = [("m", ctypes.c_int64), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
-                ("a_fmt", ctypes.c_int32), ("b_fmt", ctypes.c_int32)]
+                ("a_fmt", ctypes.c_int32), ("b_fmt", ctypes.c_int32), ("c_fmt", ctypes.c_int32)]
 
 
 EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
@@ -95,7 +98,7 @@ def lib():
                                            ctypes.c_int32, f32p, u8p, u8p, f32p, vp]
         L.mxfa_fill_normal.argtypes = [f32p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp]
         L.mxfa_kv_append.argtypes = [P(KvParams), f32p, f32p, ctypes.c_int32, ctypes.c_int32] + [u8p] * 4 + [f32p, vp]
-        L.mxfa_gemm.argtypes = [P(GemmParams), u8p, u8p, u8p, u8p, f32p, vp]
+        L.mxfa_gemm.argtypes = [P(GemmParams), u8p, u8p, u8p, u8p, vp, vp]
         L.mxfa_status_string.argtypes = [ctypes.c_int]
         L.mxfa_status_string.restype = ctypes.c_char_p
         L.mxfa_last_error.restype = ctypes.c_char_p
@@ -183,18 +186,21 @@ def softmax_requant(s, row_max, c, p_rule=P_R1, stream=None):
     return p, codes, scales, row_sum
 
 
-def gemm(a, a_sc, b, b_sc, a_fmt=FMT_E4M3, b_fmt=FMT_E4M3, out=None, stream=None):
+def gemm(a, a_sc, b, b_sc, a_fmt=FMT_E4M3, b_fmt=FMT_E4M3, out=None, stream=None, c_fmt=C_F32):
     """MX GEMM (mxfa_gemm): a [M][K] and b [K][N] uint8 codes, a_sc [K/32][M] and
-    b_sc [K/32][N] E8M0 codes (CUDA tensors) -> C [M][N] float32."""
+    b_sc [K/32][N] E8M0 codes (CUDA tensors) -> C [M][N] float32 (c_fmt C_F32) or
+    bfloat16 (C_BF16)."""
     import torch
     M, K = a.shape
     N = b.shape[1]
     for t in (a, a_sc, b, b_sc):
         assert t.is_cuda and t.dtype == torch.uint8 and t.is_contiguous()
     assert b.shape[0] == K and tuple(a_sc.shape) == (K // 32, M) and tuple(b_sc.shape) == (K // 32, N)
+    dt = torch.bfloat16 if c_fmt == C_BF16 else torch.float32
     if out is None:
-        out = torch.empty((M, N), dtype=torch.float32, device=a.device)
-    p = GemmParams(M, N, K, int(a_fmt), int(b_fmt))
+        out = torch.empty((M, N), dtype=dt, device=a.device)
+    assert out.dtype == dt and out.is_contiguous() and tuple(out.shape) == (M, N)
+    p = GemmParams(M, N, K, int(a_fmt), int(b_fmt), int(c_fmt))
     _check(lib().mxfa_gemm(ctypes.byref(p), _ptr(a), _ptr(a_sc), _ptr(b), _ptr(b_sc), _ptr(out), _stream(stream)))
     return out
 

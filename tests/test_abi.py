@@ -138,7 +138,7 @@ def test_gemm_argument_validation():
     ptr = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
     for bad, status in ((G(0, 64, 64, 0, 0), 1), (G(64, 64, 48, 0, 0), 1), (G(64, 64, 96, 0, 0), 2),
                         (G(40, 64, 64, 0, 0), 2), (G(64, 64, 64, 3, 0), 1), (G(1 << 20, 64, 1 << 12, 0, 0), 2),
-                        (G(64, 1 << 22, 64, 0, 0), 2)):
+                        (G(64, 1 << 22, 64, 0, 0), 2), (G(64, 64, 64, 0, 0, 2), 1)):
         assert L.mxfa_gemm(ctypes.byref(bad), ptr, ptr, ptr, ptr, ptr, None) == status
     ok = G(64, 64, 64, 0, 0)
     assert L.mxfa_gemm(ctypes.byref(ok), None, ptr, ptr, ptr, ptr, None) == 1

@@ -79,6 +79,22 @@ def test_gemm_real_data_and_requant():
     np.testing.assert_array_equal(np_(codes), oc)
 
 
+def test_gemm_bf16_output_is_rne_of_fp32():
+    """c_fmt = C_BF16 writes the same accumulators rounded to bf16 (nearest even): bit-equal
+    to torch's fp32 -> bf16 conversion of the fp32 output, ragged shapes included."""
+    for M, N, K, seed in ((256, 256, 512, 21), (272, 528, 320, 22)):
+        rng = np.random.default_rng(seed)
+        a, b = _codes(rng, (M, K), 0), _codes(rng, (K, N), 0)
+        sa = rng.integers(112, 142, (K // 32, M)).astype(np.uint8)
+        sb = rng.integers(112, 142, (K // 32, N)).astype(np.uint8)
+        dev = [torch.from_numpy(x).to(DEV) for x in (a, sa, b, sb)]
+        c32 = mxfa.gemm(*dev)
+        c16 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+        mxfa.gemm(*dev, out=c16, c_fmt=mxfa.C_BF16)
+        torch.cuda.synchronize()
+        assert torch.equal(c16.view(torch.int16), c32.to(torch.bfloat16).view(torch.int16))
+
+
 def test_gemm_deterministic():
     rng = np.random.default_rng(5)
     a, b = _codes(rng, (256, 512), 0), _codes(rng, (512, 256), 0)
