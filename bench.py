@@ -33,6 +33,15 @@ def decode_config():
     return dict(B=64, Hq=32, Hkv=8, L=8192, D=128)
 
 
+# The other prefill configs of BASELINE.json (timed for the roofline table; the headline is
+# configs[2]).  N(0,1) inputs; c4 is the gemma variant (window, softcap, E3M2 V).
+OTHER_CONFIGS = {
+    "c1": dict(B=1, Hq=1, Hkv=1, S=256, D=64, causal=False, outlier_p=0.0),
+    "c2": dict(B=4, Hq=16, Hkv=16, S=2048, D=128, causal=True, outlier_p=0.0),
+    "c4": dict(B=1, Hq=16, Hkv=8, S=8192, D=256, causal=True, outlier_p=0.0, window=4096, softcap=50.0, v_e3m2=True),
+}
+
+
 def make_prefill(torch, mxfa, c, seed=1):
     dev = "cuda:0"
     Q = torch.empty((c["B"], c["Hq"], c["S"], c["D"]), dtype=torch.float32, device=dev)
@@ -40,12 +49,47 @@ def make_prefill(torch, mxfa, c, seed=1):
     V = torch.empty_like(K)
     for i, X in enumerate((Q, K, V)):
         mxfa.fill_normal(X, seed * 3 + i, c["outlier_p"], 20.0)
+    vf = mxfa.FMT_E3M2 if c.get("v_e3m2") else mxfa.FMT_E4M3
     q, qs = mxfa.quantize_rows(Q)
     k, ks = mxfa.quantize_rows(K)
-    v, vs = mxfa.quantize_cols(V)
+    v, vs = mxfa.quantize_cols(V, vf)
     del Q, K, V
-    p = mxfa.make_params(c["B"], c["Hq"], c["Hkv"], c["S"], c["S"], c["D"], causal=c["causal"])
+    p = mxfa.make_params(c["B"], c["Hq"], c["Hkv"], c["S"], c["S"], c["D"], causal=c["causal"],
+                         window=c.get("window", 0), softcap=c.get("softcap", 0.0), v_fmt=vf)
     return p, (q, qs, k, ks, v, vs)
+
+
+def bench_other_configs(torch, mxfa, args):
+    """configs[0], [1], [3]: TFLOP/s and the roofline fraction max(F/P_mfma, B/BW_hbm) / t,
+    B = codes + scales read once + fp32 O written once (E3M2 V counted at 6 bits)."""
+    res = {}
+    for name, c in OTHER_CONFIGS.items():
+        p, ops = make_prefill(torch, mxfa, c, seed=7)
+        out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device="cuda:0")
+        ms = time_calls(torch, lambda: mxfa.prefill(p, *ops, out=out), max(20, args.steps // 4), args.warmup)
+        flops = mxfa.attention_flops(p)
+        vbytes = ops[4].numel() * (0.75 if c.get("v_e3m2") else 1.0)
+        nbytes = sum(t.numel() for t in (ops[0], ops[1], ops[2], ops[3], ops[5])) + vbytes + out.numel() * 4
+        t = ms * 1e-3
+        frac = max(flops / (MXFP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) / t
+        res[name] = {"shape": f"B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} S={c['S']} D={c['D']}"
+                              + (" causal" if c["causal"] else "") + (f" window={c['window']}" if c.get("window") else "")
+                              + (f" softcap={c['softcap']}" if c.get("softcap") else "") + (" V=E3M2" if c.get("v_e3m2") else ""),
+                     "ms_per_call": round(ms, 4), "tflops": round(flops / t / 1e12, 1),
+                     "gflop": round(flops / 1e9, 3), "mb": round(nbytes / 1e6, 1), "roofline_frac": round(frac, 4)}
+        del ops, out
+    return res
+
+
+def hbm_copy_gbs(torch):
+    """Measured device-to-device copy rate (read + write bytes per second), 1 GiB."""
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    ms = time_calls(torch, lambda: b.copy_(a), 20, 3)
+    del a, b
+    return round(2 * n / (ms * 1e-3) / 1e9, 1)
 
 
 PREHEAT_S = 0.25
@@ -262,8 +306,14 @@ def main():
                             "bytes_per_call": nbytes, "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
     if not args.no_decode:
+        result["decode"]["hbm_copy_gbs"] = hbm_copy_gbs(torch)
         result["kv_append"] = bench_kv_append(torch, mxfa, args)
         result["gemm"] = bench_gemm(torch, mxfa, args)
+        result["other_configs"] = bench_other_configs(torch, mxfa, args)
+    props = torch.cuda.get_device_properties(0)
+    result["device"] = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
+                        "compute_units": props.multi_processor_count,
+                        "memory_gib": round(props.total_memory / 2 ** 30, 1)}
 
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
