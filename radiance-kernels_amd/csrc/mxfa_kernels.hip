@@ -422,6 +422,40 @@ __device__ __forceinline__ void load_block(BlockRegs<D>& r, const uint8_t* __res
   }
 }
 
+// The same loads through buffer resources over one (b, KV head)'s K, K scales, V and V
+// scales, built once per workgroup and bounded at Sk keys (a load at a key >= Sk reads
+// 0): the per-block cost is one offset add instead of building four resources (1.4%
+// faster at D = 128; at D = 256, one wave per SIMD, the per-block resources are faster).
+struct KvRsrc {
+  __amdgpu_buffer_rsrc_t k, ks, v, vs;
+};
+
+template <int D>
+__device__ __forceinline__ KvRsrc kv_rsrc(const uint8_t* kb, const uint8_t* ksb, const uint8_t* vb, const uint8_t* vsb,
+                                          int Sk) {
+  KvRsrc r;
+  r.k = buf_rsrc(kb, 0, (int64_t)Sk * D);
+  r.ks = buf_rsrc(ksb, 0, (int64_t)Sk * (D / 32));
+  r.v = buf_rsrc(vb, 0, (int64_t)Sk * D);
+  r.vs = buf_rsrc(vsb, 0, (int64_t)(Sk / 32) * D);
+  return r;
+}
+
+template <int D>
+__device__ __forceinline__ void load_block(BlockRegs<D>& r, const KvRsrc& rs, int key0, int tid) {
+  constexpr int CPR = BlockRegs<D>::CPR;
+#pragma unroll
+  for (int i = 0; i < BlockRegs<D>::PER; i++) {
+    const int c = tid + i * NWAVE * 64;
+    const int row = c / CPR, col = (c % CPR) * 16;
+    r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, (key0 + row) * D + col, 0, 0);
+    r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.v, (key0 + row) * D + col, 0, 0);
+    r.kscale[i] = __builtin_amdgcn_raw_buffer_load_b8(rs.ks, (key0 + row) * (D / 32) + col / 32, 0, 0);
+  }
+  constexpr int SCH = BlockRegs<D>::SCH;
+  if (tid < SCH) r.vsc = __builtin_amdgcn_raw_buffer_load_b128(rs.vs, (key0 / 32) * D + tid * 16, 0, 0);  // [key/32][D]
+}
+
 // Registers -> LDS: K dequantized to bf16, V codes (E3M2 widened to E4M3), V scales.
 template <int D>
 __device__ __forceinline__ void store_block(const BlockRegs<D>& r, uint8_t* sKb, uint8_t* sV, uint8_t* sVs, int tid,
@@ -822,16 +856,17 @@ __device__ void prefill_impl(const FaArgs& a) {
     }
   };
   if constexpr (D <= 128) {
+    const KvRsrc rs = kv_rsrc<D>(kb, ksb, vb, vsb, a.Sk);
     // Two register stages: block j+1 is loaded during iteration j-1 and stored to LDS at
     // the end of iteration j, so each global load has a whole iteration to land.
     BlockRegs<D> ra, rb;
-    if (j0 < j1) load_block<D>(ra, kb, ksb, vb, vsb, j0 * BN, a.Sk, tid);
-    if (j0 + 1 < j1) load_block<D>(rb, kb, ksb, vb, vsb, (j0 + 1) * BN, a.Sk, tid);
+    if (j0 < j1) load_block<D>(ra, rs, j0 * BN, tid);
+    if (j0 + 1 < j1) load_block<D>(rb, rs, (j0 + 1) * BN, tid);
     if (j0 < j1) store_block<D>(ra, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
     __syncthreads();
     auto step = [&](int j, BlockRegs<D>& nxt2, const BlockRegs<D>& nxt1) {
       const int buf = (j - j0) & 1;
-      if (j + 2 < j1) load_block<D>(nxt2, kb, ksb, vb, vsb, (j + 2) * BN, a.Sk, tid);
+      if (j + 2 < j1) load_block<D>(nxt2, rs, (j + 2) * BN, tid);
       compute(j, buf);
       if (j + 1 < j1) store_block<D>(nxt1, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
       __syncthreads();
