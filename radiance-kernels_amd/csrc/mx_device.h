@@ -57,6 +57,21 @@ __device__ __forceinline__ uint32_t scale_code_p(float amax) {
   return s < 0 ? 0u : (uint32_t)s;
 }
 
+// The same code with a fast path for the attention P tiles: the round-up term of
+// scale_code_p (floorf(log2f()) = e + 1) needs a mantissa of at least 2^23 - 0x2c, so when
+// no lane of the wave has one the code is max(exponent field - 8, 0); otherwise the whole
+// wave takes the closed form.  Wave-uniform branch; the result equals scale_code_p.
+__device__ __forceinline__ uint32_t scale_code_p_fast(float amax) {
+  const uint32_t b = __float_as_uint(amax);
+  const int s = (int)(b >> 23) - 8;
+  uint32_t sc = (uint32_t)(s < 0 ? 0 : s);
+  if (__builtin_expect(__any((b & 0x7fffffu) >= 0x7fffd4u), 0)) {
+    __asm__ volatile("");          // keeps the closed form behind the branch
+    sc = scale_code_p(amax);
+  }
+  return sc;
+}
+
 // R1 E4M3 element code of an already scaled value (integer formulation).
 __device__ __forceinline__ uint32_t e4m3_code(float y) {
   uint32_t b = __float_as_uint(y);
@@ -186,10 +201,14 @@ struct PTileBounds {
   float flush, cap, scale;
 };
 
+// flush = F4M3 * 2^(sc - 127) for sc >= 8, as the bit pattern (sc << 23) + (F4M3 bits -
+// (127 << 23)) in wrapping 32-bit arithmetic.  For sc < 8 the same expression gives a
+// negative float, a NaN pattern or (sc = 7) a subnormal below 2^-126, and no P >= 0 is
+// below it except 0 itself (an exponential returns no subnormals): no flush, as R1 wants.
 __device__ __forceinline__ PTileBounds p_tile_bounds(uint32_t sc) {
   const uint32_t sh = 127u - sc;
   PTileBounds b;
-  b.flush = __uint_as_float(sc >= 8u ? kE4M3FlushBits - (sh << 23) : 0u);
+  b.flush = __uint_as_float((sc << 23) + (kE4M3FlushBits - (127u << 23)));
   b.cap = __uint_as_float(k448Bits - (sh << 23));
   b.scale = __uint_as_float((sc << 23) | 0x400000u);
   return b;
@@ -207,12 +226,22 @@ __device__ __forceinline__ uint32_t cvt_pack4(float y0, float y1, float y2, floa
   pk = __builtin_nondeterministic_value(pk);        // both halves are written below
   pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, y0, y1, scale, false);
   pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, y2, y3, scale, true);
-  return (uint32_t)(uint16_t)pk[0] | ((uint32_t)(uint16_t)pk[1] << 16);
+  return __builtin_bit_cast(uint32_t, pk);
+}
+
+// The same, with the first conversion writing into y0's register (no longer needed once
+// converted), which spares the register clear the form above gets (R1 P tiles; with the
+// R2 tiles it measured slower).
+__device__ __forceinline__ uint32_t cvt_pack4_in_place(float y0, float y1, float y2, float y3, float scale) {
+  v2s_t pk = __builtin_bit_cast(v2s_t, y0);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, y0, y1, scale, false);
+  pk = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(pk, y2, y3, scale, true);
+  return __builtin_bit_cast(uint32_t, pk);
 }
 
 // Four P values (>= 0, finite) of one tile -> their R1 E4M3 codes (byte i = value i).
 __device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
-  return cvt_pack4(p_bound(p0, b), p_bound(p1, b), p_bound(p2, b), p_bound(p3, b), b.scale);
+  return cvt_pack4_in_place(p_bound(p0, b), p_bound(p1, b), p_bound(p2, b), p_bound(p3, b), b.scale);
 }
 
 // ---------------------------------------------------------------------------

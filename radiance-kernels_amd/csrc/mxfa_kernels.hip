@@ -507,7 +507,7 @@ __device__ __forceinline__ void key_limits(const FaArgs& a, int qpos, bool qvali
 // exp2(fma(s, c, -m*c)); fma and exp2 are monotone, so no P of the tile exceeds the amax
 // by more than one rounding residue, which leaves its code unchanged.
 __device__ __forceinline__ uint32_t p_tile_scale(float bmax, float mu, float c) {
-  return scale_code_p(__builtin_amdgcn_exp2f((bmax - mu) * c));
+  return scale_code_p_fast(__builtin_amdgcn_exp2f((bmax - mu) * c));
 }
 
 // 16 P values of one lane: writes P and the codes (w[g] byte j = value 4g + j), adds
