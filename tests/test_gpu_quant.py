@@ -145,6 +145,41 @@ def test_softmax_requant_bit_exact(c):
     np.testing.assert_allclose(rsum, p.astype(np.float64).sum(axis=1), rtol=1e-5, atol=1e-30)
 
 
+def test_softmax_requant_scale_log2f_window():
+    """Tile maxima a few ulps below -k (k = 0..30, exponent argument units, c = 1, row max 0):
+    the tile amax 2^(max s) then sits within a few dozen ulps below a power of two, the band
+    where floorf(log2f()) may round up and the kernels' scale code leaves its fast path for
+    the closed form.  With c = 1 the device's tile amax is exactly the P of the tile's max
+    element, so the scale must be R1's code of that P bit for bit, and the element codes
+    R1's codes under that scale."""
+    rng = np.random.default_rng(303)
+    rows, cols = 4096, 128
+    nb = cols // 32
+    k = rng.integers(0, 31, size=(rows, nb)).astype(np.float32)
+    ulps = rng.integers(1, 6, size=(rows, nb)).astype(np.uint32)
+    tmax = ((-k).view(np.uint32) + ulps).view(np.float32)           # a few ulps below -k
+    tmax[k == 0] = -np.float32(2.0 ** -24) * ulps[k == 0].astype(np.float32)
+    plain = rng.random((rows, nb)) < 0.3                            # tiles far from the window
+    tmax[plain] = -rng.uniform(0.1, 20.0, size=plain.sum()).astype(np.float32)
+    s = (tmax[:, :, None] - rng.uniform(0.0, 30.0, size=(rows, nb, 32)).astype(np.float32)).astype(np.float32)
+    pos = rng.integers(0, 32, size=(rows, nb))
+    np.put_along_axis(s, pos[:, :, None], tmax[:, :, None], axis=2)
+    s = np.ascontiguousarray(s.reshape(rows, cols))
+    rmax = np.zeros(rows, np.float32)
+    p, codes, scales, rsum = mxfa.softmax_requant(torch.from_numpy(s).to(DEV), torch.from_numpy(rmax).to(DEV), 1.0)
+    p, codes, scales = (np_(t) for t in (p, codes, scales))
+    pmax = p.reshape(rows, nb, 32).max(axis=2)
+    L = O.lib()
+    ref = np.array([[L.orc_scale_code(float(a), O.FMT_E4M3) for a in r] for r in pmax], np.uint8)
+    bad = np.argwhere(scales != ref)
+    assert len(bad) == 0, [(float(pmax[i, j]), int(scales[i, j]), int(ref[i, j])) for i, j in bad[:8]]
+    band = (pmax.view(np.uint32) & 0x7FFFFF) >= 0x7FFFD4            # tiles that take the closed form
+    assert band.sum() > 1000 and (~band).sum() > 1000
+    sh = 127 - np.repeat(scales.astype(np.int32), 32, axis=1)
+    want = O.e4m3_encode(np.ldexp(p, sh).astype(np.float32))
+    assert np.array_equal(codes, want)
+
+
 @pytest.mark.parametrize("c", [0.08838834764831845 * LOG2E, 1.0])
 def test_softmax_requant_r2_bit_exact(c):
     """Rule R2 on the device: P is bf16 (low half zero), the codes are exactly the oracle's
