@@ -186,19 +186,22 @@ __device__ __forceinline__ uint32_t e3m2x4_to_e4m3x4(uint32_t w) {
 // ---------------------------------------------------------------------------
 // R1 requant of the attention P tiles without rescaling P first.  With sh = 127 - sc,
 // R1 encodes y = P * 2^sh: zero below F4M3 (the smallest float whose floorf(log2f())
-// is >= -6), 448 from 448 up, RNE on the E4M3 grid in between.  The per-tile bounds
-// are moved to the P side (exact power-of-two scalings): flush below F4M3 * 2^-sh --
-// for sh >= 120 that bound is below 2^-126 and no nonzero P of an exponential (which
-// returns 0 below 2^-126) reaches it -- and cap at 448 * 2^-sh.  The conversion then
-// divides by its scale operand; it uses only that operand's exponent field (measured on
-// gfx950: 1.5 acts as 1, 3.0 as 2, and a float with exponent field 0 as 2^-127), so
-// (sc << 23) | 0x400000 is 2^(sc - 127) for every code, sc = 0 included.
+// is >= -6), 448 from 448 up, RNE on the E4M3 grid in between.  The flush bound is moved
+// to the P side (an exact power-of-two scaling): zero below F4M3 * 2^-sh -- for sh >= 120
+// that bound is below 2^-126 and no nonzero P of an exponential (which returns 0 below
+// 2^-126) reaches it.  The conversion then divides by its scale operand; it uses only that
+// operand's exponent field (measured on gfx950: 1.5 acts as 1, 3.0 as 2, and a float with
+// exponent field 0 as 2^-127), so (sc << 23) | 0x400000 is 2^(sc - 127) for every code,
+// sc = 0 included.  The 448 saturation is applied to the packed codes: the conversion has
+// no saturating form and returns 0x7f for a scaled value above 464 (values in (448, 464]
+// round to 448); a P never exceeds its tile amax by more than a rounding residue and the
+// amax scales into [256, 512), so every code is at most 0x7f and 0x7f -> 0x7e is exactly
+// R1's saturation (three instructions per four codes instead of a min per value).
 // ---------------------------------------------------------------------------
 constexpr uint32_t kE4M3FlushBits = (120u << 23) | 0x7ffffeu;   // F4M3
-constexpr uint32_t k448Bits = 0x43e00000u;
 
 struct PTileBounds {
-  float flush, cap, scale;
+  float flush, scale;
 };
 
 // flush = F4M3 * 2^(sc - 127) for sc >= 8, as the bit pattern (sc << 23) + (F4M3 bits -
@@ -206,19 +209,15 @@ struct PTileBounds {
 // negative float, a NaN pattern or (sc = 7) a subnormal below 2^-126, and no P >= 0 is
 // below it except 0 itself (an exponential returns no subnormals): no flush, as R1 wants.
 __device__ __forceinline__ PTileBounds p_tile_bounds(uint32_t sc) {
-  const uint32_t sh = 127u - sc;
   PTileBounds b;
   b.flush = __uint_as_float((sc << 23) + (kE4M3FlushBits - (127u << 23)));
-  b.cap = __uint_as_float(k448Bits - (sh << 23));
   b.scale = __uint_as_float((sc << 23) | 0x400000u);
   return b;
 }
 
 typedef short v2s_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ float p_bound(float p, const PTileBounds& b) {
-  return __builtin_fminf(p < b.flush ? 0.0f : p, b.cap);
-}
+__device__ __forceinline__ float p_flush(float p, const PTileBounds& b) { return p < b.flush ? 0.0f : p; }
 
 // Four already bounded values of one tile -> their E4M3 codes (byte i = value i).
 __device__ __forceinline__ uint32_t cvt_pack4(float y0, float y1, float y2, float y3, float scale) {
@@ -239,9 +238,12 @@ __device__ __forceinline__ uint32_t cvt_pack4_in_place(float y0, float y1, float
   return __builtin_bit_cast(uint32_t, pk);
 }
 
-// Four P values (>= 0, finite) of one tile -> their R1 E4M3 codes (byte i = value i).
+// Four P values (>= 0, finite, at most the tile amax) of one tile -> their R1 E4M3 codes
+// (byte i = value i).
 __device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
-  return cvt_pack4_in_place(p_bound(p0, b), p_bound(p1, b), p_bound(p2, b), p_bound(p3, b), b.scale);
+  const uint32_t w = cvt_pack4_in_place(p_flush(p0, b), p_flush(p1, b), p_flush(p2, b), p_flush(p3, b), b.scale);
+  const uint32_t top = (w + 0x01010101u) >> 7;     // bit 0 of each byte: that byte was 0x7f
+  return w & ~(top & 0x01010101u);
 }
 
 // ---------------------------------------------------------------------------
