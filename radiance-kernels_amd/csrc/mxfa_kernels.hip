@@ -1017,7 +1017,12 @@ __device__ void decode_split_impl(const FaArgs& a) {
         ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, so, 0, 0);
     }
   };
-  // V codes and scales of a block (stored to the wave's LDS slot after its scores)
+  // V codes and scales of a block (stored to the wave's LDS slot after its scores).  Read
+  // once per call, whole lines per instruction: non-temporal loads (cache policy nt) —
+  // measured on c5, 11% faster than the default policy.  K keeps the default: each K
+  // instruction covers 32 bytes of every 128-byte line (a lane holds half a row), the four
+  // instructions of a row share the line through L2, and nt there costs 18%.
+  constexpr int kNonTemporal = 2;
   v4i vr[PERW];
   uint32_t vsr;
   auto load_v = [&](int key0, bool on) {
@@ -1025,10 +1030,10 @@ __device__ void decode_split_impl(const FaArgs& a) {
     for (int i = 0; i < PERW; i++) {
       const int c = lane + 64 * i;
       const uint32_t vo = on ? (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16) : 0x80000000u;
-      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0);
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kNonTemporal);
     }
     const uint32_t so = on && lane < SCW ? (uint32_t)((key0 / 32) * D + 4 * lane) : 0x80000000u;
-    vsr = __builtin_amdgcn_raw_buffer_load_b32(rvs, so, 0, 0);
+    vsr = __builtin_amdgcn_raw_buffer_load_b32(rvs, so, 0, kNonTemporal);
   };
   // one block ahead: K(j+1) goes out after the scores of block j, V(j+1) after V(j) is in
   // LDS, and both stay in flight through the softmax and PV of block j
