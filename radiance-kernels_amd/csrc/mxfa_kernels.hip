@@ -933,11 +933,11 @@ MXFA_PREFILL(256, true, P_R2, mxfa_prefill_d256_softcap_r2)
 // ---------------------------------------------------------------------------
 // Decode, D <= 128.  One wave per partial of one (b, KV head); its 32 score columns are
 // the group's query heads (columns >= group are padding).
-// K goes straight from global memory to registers in the split-d mapping and is
-// dequantized to bf16 right before each score MFMA; only V (transposed by the
-// ds_read_b64_tr_b8 reads of the PV step) passes through the wave's LDS slot.  Small
-// per-wave LDS and register footprints give two workgroups per CU, whose waves hide
-// each other's load latency.
+// K and V are read in block order (whole lines per load instruction, non-temporal) and
+// pass through the wave's LDS slot in turn: K is read back in the split-d mapping and
+// dequantized to bf16 right before each score MFMA, then V takes the slot for the
+// ds_read_b64_tr_b8 reads of the PV step.  Small per-wave LDS and register footprints
+// give two workgroups per CU, whose waves hide each other's load latency.
 // ---------------------------------------------------------------------------
 template <int D, bool SOFTCAP, int PR>
 __device__ void decode_split_impl(const FaArgs& a) {
@@ -998,31 +998,36 @@ __device__ void decode_split_impl(const FaArgs& a) {
   st.m = -INFINITY;
   st.l = 0.0f;
 
-  // this lane's K half-rows (keys key0 + 32t + r) and their E8M0 scales
-  v4i kr[NT][KC];
+  // K and V codes are read once per call, whole 128-byte lines per instruction (16 bytes
+  // per lane, consecutive lanes on consecutive bytes of a block), with non-temporal loads
+  // (cache policy nt): measured on c5, 11% faster per operand than the default policy.
+  // Loads in the split-d mapping itself (a lane reading half a key row) cover 32 bytes of
+  // each line per instruction, and nt on those costs 18%.
+  constexpr int kNonTemporal = 2;
+  // K codes of a block in block order (moved to the split-d mapping through the wave's
+  // LDS slot before the scores) and the E8M0 scales of this lane's K half-rows (keys
+  // key0 + 32t + r).  A disabled load gets an offset past every resource: it reads nothing
+  // and returns 0; no branch, so the waits on the other loads stay partial.
+  v4i kr[PERW];
   uint32_t ksr[NT];
-  // (a disabled load gets an offset past every resource: it reads nothing and returns 0;
-  // no branch, so the waits on the other loads stay partial)
   auto load_k = [&](int key0, bool on) {
+#pragma unroll
+    for (int i = 0; i < PERW; i++) {
+      const int c = lane + 64 * i;
+      const uint32_t ko = on ? (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16) : 0x80000000u;
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, kNonTemporal);
+    }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       const int row = key0 + 32 * t + r;
-      const uint32_t ko = on ? (uint32_t)(row * D + h * (D / 2)) : 0x80000000u;
       const uint32_t so = on ? (uint32_t)(D == 128 ? row * 4 + 2 * h : row * 2 + h) : 0x80000000u;
-#pragma unroll
-      for (int c = 0; c < KC; c++) kr[t][c] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * c, 0, 0);
       if constexpr (D == 128)
         ksr[t] = __builtin_amdgcn_raw_buffer_load_b16(rks, so, 0, 0);
       else
         ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, so, 0, 0);
     }
   };
-  // V codes and scales of a block (stored to the wave's LDS slot after its scores).  Read
-  // once per call, whole lines per instruction: non-temporal loads (cache policy nt) —
-  // measured on c5, 11% faster than the default policy.  K keeps the default: each K
-  // instruction covers 32 bytes of every 128-byte line (a lane holds half a row), the four
-  // instructions of a row share the line through L2, and nt there costs 18%.
-  constexpr int kNonTemporal = 2;
+  // V codes and scales of a block (stored to the wave's LDS slot after its scores)
   v4i vr[PERW];
   uint32_t vsr;
   auto load_v = [&](int key0, bool on) {
@@ -1035,25 +1040,45 @@ __device__ void decode_split_impl(const FaArgs& a) {
     const uint32_t so = on && lane < SCW ? (uint32_t)((key0 / 32) * D + 4 * lane) : 0x80000000u;
     vsr = __builtin_amdgcn_raw_buffer_load_b32(rvs, so, 0, kNonTemporal);
   };
-  // one block ahead: K(j+1) goes out after the scores of block j, V(j+1) after V(j) is in
-  // LDS, and both stay in flight through the softmax and PV of block j
+  // one block ahead: K(j+1) goes out once K(j) is in LDS, V(j+1) once V(j) is, and both
+  // stay in flight through the scores, softmax and PV of block j
   load_k(kfirst, kfirst < klast);
   load_v(kfirst, kfirst < klast);
   for (int key0 = kfirst; key0 < klast; key0 += kstride) {
-    // scores from registers: K dequantized to bf16 just before each MFMA
+    // K tile into the wave's slot (row pitch KP, like V), then each lane reads back its
+    // half-rows.  LDS operations of one wave complete in order, so the reads see the
+    // tile; the compiler barriers keep this block's K writes after the previous block's
+    // PV reads and the V writes below after these K reads (the same bytes, other lanes).
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < PERW; i++) {
+      const int c = lane + 64 * i;
+      *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = kr[i];
+    }
+    // the next block's K goes out as soon as this block's codes are in LDS (its scales
+    // replace this block's, which the scores still need: they are kept in ksc)
+    uint32_t ksc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) ksc[t] = ksr[t];
+    load_k(key0 + kstride, key0 + kstride < klast);
+    // scores: K dequantized to bf16 just before each MFMA
     v16f sc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
+      v4i kt[KC];
+#pragma unroll
+      for (int c = 0; c < KC; c++)
+        kt[c] = *reinterpret_cast<const v4i*>(&sV[wave][(32 * t + r) * KP + h * (D / 2) + 16 * c]);
       sc[t] = (v16f){};
 #pragma unroll
       for (int kk = 0; kk < D / 16; kk++) {
-        const v4i& w = kr[t][kk / 2];
-        const float scale = e8m0_as_float((ksr[t] >> (8 * (kk / 4))) & 0xffu);
+        const v4i& w = kt[kk / 2];
+        const float scale = e8m0_as_float((ksc[t] >> (8 * (kk / 4))) & 0xffu);
         const v4i ka = fp8x8_to_bf16x8((uint32_t)w[2 * (kk & 1)], (uint32_t)w[2 * (kk & 1) + 1], scale);
         sc[t] = mfma_bf16(ka, qb[kk], sc[t]);
       }
     }
-    load_k(key0 + kstride, key0 + kstride < klast);
+    __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < PERW; i++) {
       const int c = lane + 64 * i;
