@@ -372,8 +372,14 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
                                           {"mxfa_gemm_ae3m2", "mxfa_gemm_ae3m2_be3m2"}};
   const int64_t tm = (p->m + 255) / 256, tn = (p->n + 255) / 256;
   g.tiles_n = (int)tn;
+  // the kernels are built for one workgroup size (their launch bounds): 256 or 512 threads
+  const char* name = names[g.a_e3m2][g.b_e3m2];
+  int threads = 0;
+  MXFA_HIP(hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, fn_by_name(dm, name)));
+  if (threads != 256 && threads != 512)
+    return fail(MXFA_ERR_MODULE, std::string(name) + " has an unexpected workgroup size " + std::to_string(threads));
   void* args[] = {&g};
-  return launch(dm, names[g.a_e3m2][g.b_e3m2], dim3((unsigned)(tm * tn)), dim3(512), args, stream);
+  return launch(dm, name, dim3((unsigned)(tm * tn)), dim3((unsigned)threads), args, stream);
 }
 
 mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p, float outlier_mul, void* stream) {

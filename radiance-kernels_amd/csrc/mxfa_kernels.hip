@@ -1326,36 +1326,40 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_decode_combine(FaArgs a) 
 // MX GEMM: C [M][N] fp32 = sum over 32-groups g of K of 2^(SA[g][m] + SB[g][n] - 254) *
 // A[m][k] B[k][n], the operand layout of the reference's MX GEMM (A [M][K] and B [K][N]
 // codes, SA [K/32][M], SB [K/32][N]), on the scaled MXFP8 MFMA with fp32 accumulation.
-// Workgroup = 8 waves (two per SIMD) and a 256 x 256 tile of C; wave (wr, wc) owns rows
-// 128 wr .. +128 and columns 64 wc .. +64 as 4 x 2 MFMA tiles of 32 x 32.  K advances in
-// steps of 64 through two LDS stages; each thread stages 1/512 of the next step in
-// registers while the current one is multiplied.  A rows are read straight into the MFMA
-// row operand; B is read with ds_read_b64_tr_b8 (eight k rows of one column per lane).
-// Rows >= M and columns >= N read as zero and are not stored (bounded buffer resources;
-// M, N % 16 == 0).  The loop body is one basic block: E3M2 operands are a template
-// parameter (widened to E4M3 on the way into LDS, exact), the scale staging is spread over
-// all threads without branches, and the last step is peeled.
+// Workgroup = NW waves and a 256 x 256 tile of C; the waves form 2 x NW/2, and wave
+// (wr, wc) owns rows 128 wr .. +128 and 256 / (NW/2) columns as 4 x TJ MFMA tiles of
+// 32 x 32 (NW = 4: one wave per SIMD, 128 x 128 per wave, accumulators in AGPRs; NW = 8:
+// two per SIMD, 128 x 64).  K advances in steps of TK = 128 through two LDS stages; each
+// thread stages its share of the next step in registers while the current one is
+// multiplied.  A rows are read straight into the MFMA row operand; B is read with
+// ds_read_b64_tr_b8 (eight k rows of one column per lane).  Rows >= M and columns >= N
+// read as zero and are not stored (bounded buffer resources; M, N % 16 == 0).  The loop
+// body is one basic block: E3M2 operands are a template parameter (widened to E4M3 on the
+// way into LDS, exact) and the scale staging is spread over all threads without branches.
 // ---------------------------------------------------------------------------
-#ifndef MXFA_GEMM_TK
-#define MXFA_GEMM_TK 128
-#endif
 namespace gemm {
-constexpr int TM = 256, TN = 256, TK = MXFA_GEMM_TK;
+constexpr int TM = 256, TN = 256, TK = 128;
 constexpr int AP = TK + 16;                // A row pitch in LDS (bytes; conflict-free b128 rows)
 constexpr int BP = TN + 16;                // B row pitch (bytes)
 constexpr int A_BYTES = TM * AP, B_BYTES = TK * BP;
 constexpr int KB = TK / 32;                // scale blocks per step
 constexpr int S_BYTES = KB * (TM + TN);    // SA [KB][TM] then SB [KB][TN]
-constexpr int NT = 512;                    // threads per workgroup
-constexpr int CH = TK / 32;                // 16-byte chunks of A (and of B) per thread per step
-constexpr int SPT = S_BYTES / NT;          // scale bytes per thread per step
-static_assert(TM == TN && (TK == 64 || TK == 128), "tile shape");
 }  // namespace gemm
 
-struct GemmStage {
-  v4i a[gemm::CH];                         // A: 256 rows x TK B
-  v4i b[gemm::CH];                         // B: TK rows x 256 B
-  uint32_t s;                              // SPT scale codes (threads 0-255 SA, 256-511 SB)
+template <int NW> struct GemmCfg {
+  static constexpr int NT = 64 * NW;                               // threads per workgroup
+  static constexpr int CH = gemm::TM * gemm::TK / 16 / NT;         // 16-byte chunks of A (and of B) per thread
+  static constexpr int SPT = gemm::S_BYTES / NT;                   // scale bytes per thread per step
+  static constexpr int WCN = NW / 2;                               // wave columns
+  static constexpr int TJ = gemm::TN / WCN / 32;                   // 32-column MFMA tiles per wave
+  static_assert(NW == 4 || NW == 8, "waves per workgroup");
+  static_assert(SPT == 4 || SPT == 8, "scale staging");
+};
+
+template <int NW> struct GemmStage {
+  v4i a[GemmCfg<NW>::CH];                  // A: 256 rows x TK B
+  v4i b[GemmCfg<NW>::CH];                  // B: TK rows x 256 B
+  uint32_t s[GemmCfg<NW>::SPT / 4];        // SPT scale codes (first half of the threads SA, second SB)
 };
 
 struct GemmRes {
@@ -1365,16 +1369,30 @@ struct GemmRes {
   uint32_t svoff;                          // offset of the thread's scale codes within a k-step
 };
 
-// Everything at k >= K reads as zero (E8M0 code 0 = 2^-127 scales, so such a step, or the
-// part of one past K when K % TK == 64, adds exact zeros): A chunks past K get an offset
-// outside the resource, the B and scale resources end at K.
-__device__ __forceinline__ void gemm_load(GemmStage& r, const GemmArgs& g, const GemmRes& res, int n0, int k0, int tid) {
+template <int NW>
+__device__ __forceinline__ void gemm_load_scales(GemmStage<NW>& r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, int soff) {
+  if constexpr (GemmCfg<NW>::SPT == 4) {
+    r.s[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0);
+  } else {
+    const auto t = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
+    r.s[0] = t[0];
+    r.s[1] = t[1];
+  }
+}
+
+// Everything at k >= K reads as zero (E8M0 code 0 = 2^-127 scales, so the part of a step
+// past K when K % TK == 64 adds exact zeros): A chunks past K get an offset outside the
+// resource, the B and scale resources end at K.
+template <int NW>
+__device__ __forceinline__ void gemm_load(GemmStage<NW>& r, const GemmArgs& g, const GemmRes& res, int n0, int k0,
+                                          int tid) {
   using namespace gemm;
+  using C = GemmCfg<NW>;
   const int krem = max(0, min(TK, g.K - k0));                   // rows of this step below K
   const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, (int64_t)k0 * g.N, (int64_t)krem * g.N);
 #pragma unroll
-  for (int i = 0; i < CH; i++) {
-    const int c = tid + NT * i;
+  for (int i = 0; i < C::CH; i++) {
+    const int c = tid + C::NT * i;
     const int row = c / (TK / 16), col = (c % (TK / 16)) * 16;  // A chunk: row, 16-byte column
     r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, col < krem ? (uint32_t)(row * g.K + k0 + col) : 0x80000000u,
                                                    0, 0);
@@ -1382,19 +1400,57 @@ __device__ __forceinline__ void gemm_load(GemmStage& r, const GemmArgs& g, const
     const uint32_t bo = n0 + bc < g.N ? (uint32_t)(kr * g.N + n0 + bc) : 0x80000000u;
     r.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, bo, 0, 0);
   }
-  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, (int64_t)(krem / 32) * res.sdim);
-  if constexpr (SPT == 4)
-    r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, res.svoff, 0, 0);
-  else
-    r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, res.svoff, 0, 0);
+  gemm_load_scales<NW>(r, buf_rsrc(res.sbase, (int64_t)(k0 / 32) * res.sdim, (int64_t)(krem / 32) * res.sdim),
+                       res.svoff, 0);
 }
 
-template <int AE3, int BE3>
-__device__ __forceinline__ void gemm_store(const GemmStage& r, uint8_t* sA, uint8_t* sB, uint8_t* sS, int tid) {
+// When K % TK == 0 every step is whole: each thread's load offsets are fixed for the
+// whole K loop and the step enters as the scalar offset of the loads (k0 for A, k0 N for
+// B, k0 / 32 times M or N for the scales), so a step costs no address arithmetic.  Every
+// enabled load stays inside its operand (k0 <= K - TK); disabled ones (columns >= N,
+// scale columns past M or N) get a vector offset past every resource and read 0, and A
+// rows >= M are past the tile's resource.
+template <int NW> struct GemmOff {
+  uint32_t a[GemmCfg<NW>::CH];             // row K + column of the thread's A chunks
+  uint32_t b[GemmCfg<NW>::CH];             // k row N + n0 + column of its B chunks
+  __amdgpu_buffer_rsrc_t rb, rs;           // all of B, all of SA or SB
+};
+
+template <int NW>
+__device__ __forceinline__ GemmOff<NW> gemm_offsets(const GemmArgs& g, const GemmRes& res, int n0, int tid) {
   using namespace gemm;
+  using C = GemmCfg<NW>;
+  GemmOff<NW> o;
 #pragma unroll
-  for (int i = 0; i < CH; i++) {
-    const int c = tid + NT * i;
+  for (int i = 0; i < C::CH; i++) {
+    const int c = tid + C::NT * i;
+    o.a[i] = (uint32_t)((c / (TK / 16)) * g.K + (c % (TK / 16)) * 16);
+    const int kr = c >> 4, bc = (c & 15) * 16;
+    o.b[i] = n0 + bc < g.N ? (uint32_t)(kr * g.N + n0 + bc) : 0x80000000u;
+  }
+  o.rb = buf_rsrc(g.b, 0, (int64_t)g.K * g.N);
+  o.rs = buf_rsrc(res.sbase, 0, (int64_t)(g.K / 32) * res.sdim);
+  return o;
+}
+
+template <int NW>
+__device__ __forceinline__ void gemm_load_whole(GemmStage<NW>& r, const GemmRes& res, const GemmOff<NW>& o, int k0,
+                                                int N) {
+#pragma unroll
+  for (int i = 0; i < GemmCfg<NW>::CH; i++) {
+    r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(res.a, o.a[i], k0, 0);
+    r.b[i] = __builtin_amdgcn_raw_buffer_load_b128(o.rb, o.b[i], k0 * N, 0);
+  }
+  gemm_load_scales<NW>(r, o.rs, res.svoff, (k0 / 32) * res.sdim);
+}
+
+template <int NW, int AE3, int BE3>
+__device__ __forceinline__ void gemm_store(const GemmStage<NW>& r, uint8_t* sA, uint8_t* sB, uint8_t* sS, int tid) {
+  using namespace gemm;
+  using C = GemmCfg<NW>;
+#pragma unroll
+  for (int i = 0; i < C::CH; i++) {
+    const int c = tid + C::NT * i;
     v4i va = r.a[i], vb = r.b[i];
     if (AE3) {
 #pragma unroll
@@ -1407,30 +1463,32 @@ __device__ __forceinline__ void gemm_store(const GemmStage& r, uint8_t* sA, uint
     *reinterpret_cast<v4i*>(sA + (c / (TK / 16)) * AP + (c % (TK / 16)) * 16) = va;
     *reinterpret_cast<v4i*>(sB + (c >> 4) * BP + (c & 15) * 16) = vb;
   }
-  if constexpr (SPT == 4)
-    *reinterpret_cast<uint32_t*>(sS + 4 * tid) = r.s;
+  if constexpr (C::SPT == 4)
+    *reinterpret_cast<uint32_t*>(sS + 4 * tid) = r.s[0];
   else
-    *reinterpret_cast<uint16_t*>(sS + 2 * tid) = (uint16_t)r.s;
+    *reinterpret_cast<uint2*>(sS + 8 * tid) = make_uint2(r.s[0], r.s[1]);
 }
 
-// One k-step of the wave's 4 x 2 MFMA tiles from one LDS stage.
-__device__ __forceinline__ void gemm_mma(v16f (&acc)[4][2], const uint8_t* sA, const uint8_t* sB, const uint8_t* sS,
-                                         int wr, int wc, int lane) {
+// One k-step of the wave's 4 x TJ MFMA tiles from one LDS stage.
+template <int NW>
+__device__ __forceinline__ void gemm_mma(v16f (&acc)[4][GemmCfg<NW>::TJ], const uint8_t* sA, const uint8_t* sB,
+                                         const uint8_t* sS, int wr, int wc, int lane) {
   using namespace gemm;
+  constexpr int TJ = GemmCfg<NW>::TJ;
   const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
   // operands: A row tile i (rows 128 wr + 32 i + r, k = 16 h .. and 32 + 16 h ..), B
-  // column tile j (column 64 wc + 32 j + 16 (g16 & 1) + l16, k rows via transposed reads)
-  // The wave raises its priority from its first MFMA to the end of the step, so that of
-  // the two waves of a SIMD the one feeding the matrix pipe issues first while the other
-  // reads its operands (measured +2% on the c3 QKV shape; prefill is slower with it).
-  bool first = true;
+  // column tile j (column 32 TJ wc + 32 j + 16 (g16 & 1) + l16, k rows via transposed reads)
+  // With two waves per SIMD the wave raises its priority from its first MFMA to the end of
+  // the step, so that the one feeding the matrix pipe issues first while the other reads
+  // its operands (measured +2% on the c3 QKV shape; prefill is slower with it).
+  bool first = NW == 8;
 #pragma unroll
   for (int kh = 0; kh < TK / 64; kh++) {                // 64-k halves of the step
-    v8i bo[2];
-    int bsc[2];
+    v8i bo[TJ];
+    int bsc[TJ];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int ncol = 64 * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
+    for (int j = 0; j < TJ; j++) {
+      const int ncol = 32 * TJ * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int krow = 64 * kh + 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
@@ -1438,7 +1496,7 @@ __device__ __forceinline__ void gemm_mma(v16f (&acc)[4][2], const uint8_t* sA, c
         bo[j][2 * q] = t[0];
         bo[j][2 * q + 1] = t[1];
       }
-      bsc[j] = sS[KB * TM + (2 * kh + h) * TN + 64 * wc + 32 * j + r];
+      bsc[j] = sS[KB * TM + (2 * kh + h) * TN + 32 * TJ * wc + 32 * j + r];
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -1452,15 +1510,17 @@ __device__ __forceinline__ void gemm_mma(v16f (&acc)[4][2], const uint8_t* sA, c
         first = false;
       }
 #pragma unroll
-      for (int j = 0; j < 2; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
+      for (int j = 0; j < TJ; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
     }
   }
-  __builtin_amdgcn_s_setprio(0);
+  if (NW == 8) __builtin_amdgcn_s_setprio(0);
 }
 
-template <int AE3, int BE3>
+template <int NW, int AE3, int BE3>
 __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
   using namespace gemm;
+  using C = GemmCfg<NW>;
+  constexpr int TJ = C::TJ;
   __shared__ __attribute__((aligned(16))) uint8_t sA[2][A_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2][B_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t sS[2][S_BYTES];
@@ -1478,84 +1538,71 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
   const int group = item / (GM * g.tiles_n), first = group * GM, gm = min(GM, tiles_m - first);
   const int in_group = item - group * GM * g.tiles_n;
   const int m0 = (first + in_group % gm) * TM, n0 = (in_group / gm) * TN;
-  const int wr = wave >> 2, wc = wave & 3;
+  const int wr = wave / C::WCN, wc = wave % C::WCN;
 
   GemmRes res;
   res.a = buf_rsrc(g.a, (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
   {
-    // thread t stages scale codes [k0/32 + kb][c0 + SPT cp .. + SPT] of SA (t < 256) or SB;
-    // its LDS bytes are SPT t ..
-    const bool is_a = wave < 4;
-    const int t = tid & 255, kb = t / (256 / SPT), cp = t % (256 / SPT);
+    // thread t of the first (second) half of the workgroup stages scale codes
+    // [k0/32 + kb][c0 + SPT cp .. + SPT] of SA (SB); its LDS bytes are SPT t ..
+    constexpr int SPT = C::SPT, HALF = C::NT / 2;
+    const bool is_a = wave < NW / 2;                 // wave-uniform: the scale resource stays scalar
+    const int t = tid % HALF, kb = t / (256 / SPT), cp = t % (256 / SPT);
     res.sbase = is_a ? g.sa : g.sb;
     res.sdim = is_a ? g.M : g.N;
     const int c = (is_a ? m0 : n0) + SPT * cp;
     res.svoff = c < res.sdim ? (uint32_t)(kb * res.sdim + c) : 0x80000000u;
   }
 
-  v16f acc[4][2];
+  v16f acc[4][TJ];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = (v16f){};
+    for (int j = 0; j < TJ; j++) acc[i][j] = (v16f){};
 
+  // One register stage: step k + 1 is loaded while step k is multiplied, then stored into
+  // the other LDS stage.  Loads go out first and the MFMAs before the wait of the stores
+  // (the scheduler otherwise sinks the loads between the MFMAs to save registers).
   const int nk = (g.K + TK - 1) / TK;
-  if constexpr (TK == 128) {
-    // One register stage: step k + 1 is loaded while step k is multiplied, then stored
-    // into the other LDS stage.
-    GemmStage st;
-    gemm_load(st, g, res, n0, 0, tid);
-    gemm_store<AE3, BE3>(st, sA[0], sB[0], sS[0], tid);
-    __syncthreads();
+  GemmStage<NW> st;
+  gemm_load<NW>(st, g, res, n0, 0, tid);
+  gemm_store<NW, AE3, BE3>(st, sA[0], sB[0], sS[0], tid);
+  __syncthreads();
+  if (g.K % TK == 0) {
+    const GemmOff<NW> o = gemm_offsets<NW>(g, res, n0, tid);
     for (int kt = 0; kt < nk; kt++) {
       const int buf = kt & 1;
-      // loads go out first and the MFMAs before the wait of the stores (the scheduler
-      // otherwise sinks the loads between the MFMAs to save registers)
-      gemm_load(st, g, res, n0, (kt + 1) * TK, tid);
+      // the last step reloads itself (in bounds; the stage is never multiplied)
+      gemm_load_whole<NW>(st, res, o, min(kt + 1, nk - 1) * TK, g.N);
       __builtin_amdgcn_sched_barrier(0);
-      gemm_mma(acc, sA[buf], sB[buf], sS[buf], wr, wc, lane);
+      gemm_mma<NW>(acc, sA[buf], sB[buf], sS[buf], wr, wc, lane);
       __builtin_amdgcn_sched_barrier(0);
-      gemm_store<AE3, BE3>(st, sA[buf ^ 1], sB[buf ^ 1], sS[buf ^ 1], tid);
+      gemm_store<NW, AE3, BE3>(st, sA[buf ^ 1], sB[buf ^ 1], sS[buf ^ 1], tid);
       __syncthreads();
     }
   } else {
-  // Two register stages: step k + 2 is loaded while step k is multiplied and step k + 1
-  // (loaded one step earlier) goes into the other LDS stage.  The loop runs steps in
-  // pairs; for an odd step count the last step multiplies zeros.
-  GemmStage s0, s1;
-  gemm_load(s0, g, res, n0, 0, tid);
-  gemm_load(s1, g, res, n0, TK, tid);
-  gemm_store<AE3, BE3>(s0, sA[0], sB[0], sS[0], tid);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    // loads go out first and the MFMAs before the wait of the stores (the scheduler
-    // otherwise sinks the loads between the MFMAs to save registers)
-    gemm_load(s0, g, res, n0, (kt + 2) * TK, tid);
-    __builtin_amdgcn_sched_barrier(0);
-    gemm_mma(acc, sA[0], sB[0], sS[0], wr, wc, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    gemm_store<AE3, BE3>(s1, sA[1], sB[1], sS[1], tid);
-    __syncthreads();
-    gemm_load(s1, g, res, n0, (kt + 3) * TK, tid);
-    __builtin_amdgcn_sched_barrier(0);
-    gemm_mma(acc, sA[1], sB[1], sS[1], wr, wc, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    gemm_store<AE3, BE3>(s0, sA[0], sB[0], sS[0], tid);
-    __syncthreads();
-  }
+    for (int kt = 0; kt < nk; kt++) {
+      const int buf = kt & 1;
+      gemm_load<NW>(st, g, res, n0, (kt + 1) * TK, tid);
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_mma<NW>(acc, sA[buf], sB[buf], sS[buf], wr, wc, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_store<NW, AE3, BE3>(st, sA[buf ^ 1], sB[buf ^ 1], sS[buf ^ 1], tid);
+      __syncthreads();
+    }
   }
 
   // C tile: lane l, register v of tile (i, j) -> row 128 wr + 32 i + 8 (v / 4) + 4 h + v % 4,
-  // column 64 wc + 32 j + r.  Rows >= M fall outside the tile's resource; columns >= N get
-  // an offset outside every resource.  ES = bytes per C element (4 fp32, 2 bf16).
+  // column 32 TJ wc + 32 j + r.  Rows >= M fall outside the tile's resource; columns >= N
+  // get an offset outside every resource.  ES = bytes per C element (4 fp32, 2 bf16).
   const int r = lane & 31, h = lane >> 5;
   const int rows = min(TM, g.M - m0);
   const int ES = g.c_bf16 ? 2 : 4;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(g.c + (int64_t)m0 * g.N * ES), 0, (int)(uint32_t)((int64_t)rows * g.N * ES), 0x00020000);
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int n = n0 + 64 * wc + 32 * j + r;
+  for (int j = 0; j < TJ; j++) {
+    const int n = n0 + 32 * TJ * wc + 32 * j + r;
     const uint32_t cb = n < g.N ? (uint32_t)((128 * wr + 4 * h) * g.N + n) * (uint32_t)ES : 0xfffffff0u;
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -1570,7 +1617,16 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
   }
 }
 
-extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm(GemmArgs g) { gemm_impl<0, 0>(g); }
-extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_ae3m2(GemmArgs g) { gemm_impl<1, 0>(g); }
-extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_be3m2(GemmArgs g) { gemm_impl<0, 1>(g); }
-extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_ae3m2_be3m2(GemmArgs g) { gemm_impl<1, 1>(g); }
+// Waves per GEMM workgroup; the host reads the workgroup size from the kernel's
+// launch bounds (its maximum threads per block).
+#ifndef MXFA_GEMM_WAVES
+#define MXFA_GEMM_WAVES 8
+#endif
+#define MXFA_GEMM(AE, BE, NAME)                                                                         \
+  extern "C" __global__ void __launch_bounds__(64 * MXFA_GEMM_WAVES, 1) NAME(GemmArgs g) {             \
+    gemm_impl<MXFA_GEMM_WAVES, AE, BE>(g);                                                              \
+  }
+MXFA_GEMM(0, 0, mxfa_gemm)
+MXFA_GEMM(1, 0, mxfa_gemm_ae3m2)
+MXFA_GEMM(0, 1, mxfa_gemm_be3m2)
+MXFA_GEMM(1, 1, mxfa_gemm_ae3m2_be3m2)
