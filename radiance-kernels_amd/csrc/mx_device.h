@@ -72,27 +72,6 @@ __device__ __forceinline__ uint32_t scale_code_p_fast(float amax) {
   return sc;
 }
 
-// R1 E4M3 element code of an already scaled value (integer formulation).
-__device__ __forceinline__ uint32_t e4m3_code(float y) {
-  uint32_t b = __float_as_uint(y);
-  uint32_t a = b & 0x7fffffffu;
-  if (a == 0u || a >= 0x7f800000u) return 0u;
-  uint32_t s = (b >> 24) & 0x80u;
-  int E = floor_log2f(__uint_as_float(a));
-  if (E < -6) return 0u;
-  if (E > 8) return s | 0x7eu;
-  int q = 0;
-  if (E == (int)(a >> 23) - 127) {
-    uint32_t mant = a & 0x7fffffu;
-    q = (int)(mant >> 20);
-    uint32_t rem = mant & 0xfffffu;
-    q += (rem > 0x80000u || (rem == 0x80000u && (q & 1))) ? 1 : 0;
-    if (q == 8) { q = 0; E++; }
-  }
-  if (E > 8 || (E == 8 && q == 7)) return s | 0x7eu;
-  return s | ((uint32_t)(E + 7) << 3) | (uint32_t)q;
-}
-
 // Rule R4, the reference's SIMT block quantizer (kernels/simt_quant/kernel.cpp:43-117):
 // E4M3 code of y with round-half-even, saturation at 448 and subnormals kept (2^-9 grid).
 __device__ __forceinline__ uint32_t r4_round_shift(uint32_t v, int sh) {   // RNE of v / 2^sh, sh > 0
@@ -244,6 +223,30 @@ __device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float 
   const uint32_t w = cvt_pack4_in_place(p_flush(p0, b), p_flush(p1, b), p_flush(p2, b), p_flush(p3, b), b.scale);
   const uint32_t top = (w + 0x01010101u) >> 7;     // bit 0 of each byte: that byte was 0x7f
   return w & ~(top & 0x01010101u);
+}
+
+// R1 E4M3 codes of four already scaled values of any sign (byte i = value i), on the
+// hardware conversion.  R1 (lib/golden/mx_fp_math.h:205-225, restated as
+// orc_e4m3_encode in the oracle): E = floorf(log2f(|y|)); code 0 for |y| = 0, NaN, inf or
+// E < -6; 0x7e with y's sign for E > 8; otherwise the mantissa rounded to nearest even at
+// 3 bits (a carry raises E) and 0x7e for 480.  The same codes for every float:
+// - |y| below F4M3 (floorf(log2f) < -6), zeros of either sign, NaN and infinities: R1
+//   gives code 0; they are replaced by +0 before the conversion.
+// - Where floorf(log2f(|y|)) is one above the exponent of |y| (a mantissa within a few
+//   dozen ulps of the next power of two), R1 codes that power of two; round-to-nearest-
+//   even to 3 mantissa bits rounds such a mantissa (above 1.9375) up to it as well.
+// - F4M3 <= |y| < 2^-6 rounds to 2^-6 on the conversion's subnormal grid, R1's code 0x08.
+// - R1 saturates at 448 (0x7e, sign kept); the conversion rounds |y| in (448, 464] to 448
+//   and returns 0x7f / 0xff above, which is moved to 0x7e / 0xfe on the packed codes.
+__device__ __forceinline__ float r1_keep(float y) {
+  const float a = __builtin_fabsf(y);
+  return (a >= __uint_as_float(kE4M3FlushBits) && a < __builtin_inff()) ? y : 0.0f;
+}
+
+__device__ __forceinline__ uint32_t e4m3_code4(float y0, float y1, float y2, float y3) {
+  const uint32_t w = cvt_pack4(r1_keep(y0), r1_keep(y1), r1_keep(y2), r1_keep(y3), 1.0f);
+  const uint32_t top = ((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;   // that byte's low 7 bits were all 1
+  return w ^ (top >> 7);
 }
 
 // ---------------------------------------------------------------------------

@@ -57,12 +57,10 @@ template <int FMT>
 __device__ __forceinline__ uint32_t encode4(float4 v, int sh) {
   float y[4] = {__builtin_ldexpf(v.x, sh), __builtin_ldexpf(v.y, sh), __builtin_ldexpf(v.z, sh),
                 __builtin_ldexpf(v.w, sh)};
+  if (FMT == 0) return e4m3_code4(y[0], y[1], y[2], y[3]);
   uint32_t w = 0;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    uint32_t c = FMT == 0 ? e4m3_code(y[i]) : e3m2_code_bf16(bf16_rne(y[i]));
-    w |= c << (8 * i);
-  }
+  for (int i = 0; i < 4; i++) w |= e3m2_code_bf16(bf16_rne(y[i])) << (8 * i);
   return w;
 }
 
@@ -143,7 +141,7 @@ __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int r
     float y2 = __builtin_ldexpf(v.z, 127 - (int)s2), y3 = __builtin_ldexpf(v.w, 127 - (int)s3);
     uint32_t w;
     if (FMT == 0)
-      w = e4m3_code(y0) | (e4m3_code(y1) << 8) | (e4m3_code(y2) << 16) | (e4m3_code(y3) << 24);
+      w = e4m3_code4(y0, y1, y2, y3);
     else
       w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
           (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);
@@ -241,7 +239,7 @@ __device__ __forceinline__ void kv_append_v_part(const float* v_new, float* v_ta
     const float y2 = __builtin_ldexpf(x[i].z, 127 - (int)s2), y3 = __builtin_ldexpf(x[i].w, 127 - (int)s3);
     uint32_t w;
     if (FMT == 0)
-      w = e4m3_code(y0) | (e4m3_code(y1) << 8) | (e4m3_code(y2) << 16) | (e4m3_code(y3) << 24);
+      w = e4m3_code4(y0, y1, y2, y3);
     else
       w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
           (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);

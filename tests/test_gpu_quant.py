@@ -50,6 +50,40 @@ def test_quantize_rows_bit_exact(fmt):
     assert len(bad) == 0, [(float(x[i, j]), int(np_(codes)[i, j]), int(oc[i, j])) for i, j in bad[:8]]
 
 
+def test_e4m3_elements_exhaustive():
+    """Every float32 y with 2^-10 <= |y| < 512, both signs (318M values), through
+    mxfa_quantize_rows with E8M0 code 127 in every block (each 32-block leads with 256.0,
+    so y is encoded unscaled), against the oracle's R1 element rule.  Below 2^-10 R1 and the
+    conversion both give 0 (R1 flushes from F4M3 ~ 2^-6 down); from 512 up both saturate;
+    the specials (zeros, NaN, inf, overflow to inf after scaling) are in edge_rows."""
+    lo = int(np.float32(2.0 ** -10).view(np.uint32))
+    hi = int(np.float32(512.0).view(np.uint32))
+    step = 31 * (1 << 21)
+    for sign in (0, 0x80000000):
+        for start in range(lo, hi, step):
+            bits = np.arange(start, min(start + step, hi), dtype=np.uint32) | np.uint32(sign)
+            vals = bits.view(np.float32)
+            nb = -(-len(vals) // 31)
+            body = np.zeros(nb * 31, np.float32)
+            body[: len(vals)] = vals
+            x = np.empty((nb, 32), np.float32)
+            x[:, 0] = 256.0
+            x[:, 1:] = body.reshape(nb, 31)
+            codes, scales = mxfa.quantize_rows(torch.from_numpy(x).to(DEV), mxfa.FMT_E4M3)
+            oc, osc = O.quantize_rows(x, mxfa.FMT_E4M3)
+            np.testing.assert_array_equal(np_(scales), osc)
+            # code 127 (y = x) everywhere but the blocks of values just below 512, where
+            # floorf(log2f(amax)) = 9
+            assert (osc != 127).sum() <= 2
+            got = np_(codes)[:, 1:].reshape(-1)[: len(vals)]
+            want = oc[:, 1:].reshape(-1)[: len(vals)]
+            bad = np.flatnonzero(got != want)
+            assert len(bad) == 0, [(hex(int(bits[i])), int(got[i]), int(want[i])) for i in bad[:8]]
+            np.testing.assert_array_equal(np_(codes)[:, 0], oc[:, 0])
+            unscaled = np.repeat(osc[:, 0] == 127, 31)[: len(vals)]
+            np.testing.assert_array_equal(want[unscaled], O.e4m3_encode(vals[unscaled]))
+
+
 @pytest.mark.parametrize("fmt", [mxfa.FMT_E4M3, mxfa.FMT_E3M2])
 def test_quantize_cols_bit_exact(fmt):
     rng = np.random.default_rng(200 + fmt)
