@@ -799,10 +799,17 @@ __device__ void prefill_impl(const FaArgs& a) {
   // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
   // renumber them so that each XCD receives a contiguous range of work items, i.e.
   // all query blocks of the same KV head land on one XCD and share its L2.
+  // When an XCD's range holds whole heads, its heads are interleaved in dispatch order
+  // (every head's first query-block item, then every head's second, ...), so under
+  // causal masking all its heads' longest blocks start first.
   const int nwg = (int)(gridDim.x * gridDim.y);
   const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
   const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
-  const int item = xcd * per + min(xcd, rem) + (lin >> 3);
+  const int start_x = xcd * per + min(xcd, rem), cnt_x = per + (xcd < rem ? 1 : 0);
+  const int li = lin >> 3;
+  const int nh_x = cnt_x / a.n_qblk;
+  const bool whole_heads = start_x % a.n_qblk == 0 && cnt_x % a.n_qblk == 0;
+  const int item = start_x + (whole_heads ? (li % nh_x) * a.n_qblk + li / nh_x : li);
   const int qx = item % a.n_qblk, qy = item / a.n_qblk;
   const int qblk = a.causal ? (a.n_qblk - 1 - qx) : qx;   // longest rows first
   const int chunks = a.group / a.hpw;
