@@ -95,7 +95,7 @@ def hbm_copy_gbs(torch):
 PREHEAT_S = 0.25
 
 
-def time_calls(torch, fn, steps, warmup):
+def time_calls(torch, fn, steps, warmup, preheat=True):
     """Average ms per call with HIP events on the launch stream (torch's current stream).
     Untimed before the K timed calls: the W warmup calls, then more calls until at least
     PREHEAT_S seconds of them have run -- the shader clock needs about that long under load
@@ -105,7 +105,7 @@ def time_calls(torch, fn, steps, warmup):
         fn()
     torch.cuda.synchronize()
     t0 = time.time()
-    while time.time() - t0 < PREHEAT_S:
+    while preheat and time.time() - t0 < PREHEAT_S:
         for _ in range(8):
             fn()
         torch.cuda.synchronize()
@@ -205,10 +205,35 @@ def bench_gemm(torch, mxfa, args):
                          "frac_mxfp8_peak": round(tf16 / MXFP8_PEAK_TFLOPS, 4)}}
 
 
-def cpu_baseline(mxfa, p, ops_host, threads):
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# Host threads of the CPU baseline: every core this process may run on, up to the 16 host
+# threads that one GPU's share of the GPU box comes with (the box runs other GPUs' jobs on
+# the rest, whatever the cpu count reports).
+CPU_THREAD_CAP = 16
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, CPU_THREAD_CAP)), n
+
+
+def cpu_baseline(mxfa, p, ops_host, threads, visible):
     """The CPU oracle (this repo's C restatement of the reference algorithm, threaded over
     query heads) on the whole configs[2] workload: every (batch, query head), the same
-    block size.  About 40 thread-seconds of CPU work on 16 threads."""
+    block size.  About 40 thread-seconds of CPU work."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     op = O.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim,
@@ -218,8 +243,48 @@ def cpu_baseline(mxfa, p, ops_host, threads):
     dt = time.time() - t0
     flops = mxfa.attention_flops(p)
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "cpus_visible": visible,
             "sample": f"all of configs[2]: {p.batch} x {p.num_q_heads} query heads ({flops / 1e9:.1f} GFLOP, "
-                      f"{dt:.2f} s wall on {threads} threads)"}
+                      f"{dt:.2f} s wall on {threads} threads of {visible} visible; the GPU box gives one GPU "
+                      f"{CPU_THREAD_CAP} host threads)"}
+
+
+def profile_workload(torch, mxfa, name, args):
+    """Run one workload alone, for rocprofv3: W untimed calls, then K calls timed with HIP
+    events on the launch stream.  Prints one JSON line."""
+    dev = "cuda:0"
+    if name in ("c3", "c3r2"):
+        p, ops = make_prefill(torch, mxfa, prefill_config())
+        if name == "c3r2":
+            p.p_rule = mxfa.P_R2
+    elif name in OTHER_CONFIGS:
+        p, ops = make_prefill(torch, mxfa, OTHER_CONFIGS[name], seed=7)
+    elif name == "decode":
+        dc = decode_config()
+        Qd = torch.empty((dc["B"], dc["Hq"], 1, dc["D"]), dtype=torch.float32, device=dev)
+        Kd = torch.empty((dc["B"], dc["Hkv"], dc["L"], dc["D"]), dtype=torch.float32, device=dev)
+        mxfa.fill_normal(Qd, 11)
+        mxfa.fill_normal(Kd, 12)
+        qd, qsd = mxfa.quantize_rows(Qd)
+        kd, ksd = mxfa.quantize_rows(Kd)
+        mxfa.fill_normal(Kd, 13)
+        vd, vsd = mxfa.quantize_cols(Kd)
+        del Kd
+        pd = mxfa.make_params(dc["B"], dc["Hq"], dc["Hkv"], 1, dc["L"], dc["D"], causal=True, q_pos0=dc["L"] - 1)
+        _, ws_bytes = mxfa.decode_plan(pd)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        od = torch.empty((dc["B"], dc["Hq"], 1, dc["D"]), dtype=torch.float32, device=dev)
+        ms = time_calls(torch, lambda: mxfa.decode(pd, qd, qsd, kd, ksd, vd, vsd, out=od, workspace=ws),
+                        args.steps, args.warmup, preheat=False)
+        print(json.dumps({"profile": name, "ms_per_call": round(ms, 4), "calls": args.steps + args.warmup}), flush=True)
+        return
+    else:
+        raise SystemExit(f"bench.py: unknown --profile workload {name!r}")
+    out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device=dev)
+    ms = time_calls(torch, lambda: mxfa.prefill(p, *ops, out=out), args.steps, args.warmup, preheat=False)
+    flops = mxfa.attention_flops(p)
+    print(json.dumps({"profile": name, "ms_per_call": round(ms, 4), "calls": args.steps + args.warmup,
+                      "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}), flush=True)
 
 
 def main():
@@ -230,6 +295,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="only run a 256 MiB device copy x3")
+    ap.add_argument("--profile", metavar="WORKLOAD",
+                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode): W untimed + K timed calls")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in DESIGN.md)",
@@ -243,6 +310,9 @@ def main():
         return
     import mxfa
     mxfa.init()
+    if args.profile:
+        profile_workload(torch, mxfa, args.profile, args)
+        return
 
     c = prefill_config()
     p, ops = make_prefill(torch, mxfa, c)
@@ -316,9 +386,9 @@ def main():
                         "memory_gib": round(props.total_memory / 2 ** 30, 1)}
 
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads, visible = cpu_threads()
         host = [t.cpu().numpy() for t in ops]
-        result["cpu_baseline"] = cpu_baseline(mxfa, p, host, threads)
+        result["cpu_baseline"] = cpu_baseline(mxfa, p, host, threads, visible)
 
     print(json.dumps(result), flush=True)
 

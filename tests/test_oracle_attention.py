@@ -154,20 +154,111 @@ def test_fully_masked_rows_are_zero():
 
 
 def test_softcap_limits():
+    """cap -> infinity is the uncapped recurrence."""
     B, H, S, D = 1, 2, 64, 64
     Q, K, V = normal_inputs(B, H, H, S, S, D, seed=10)
     ops = quantize_qkv(Q, K, V)
     p0 = O.make_params(B, H, H, S, S, D, causal=True)
     pbig = O.make_params(B, H, H, S, S, D, causal=True, softcap=1e12)
     np.testing.assert_allclose(O.attention(pbig, *ops, block_n=32), O.attention(p0, *ops, block_n=32), rtol=1e-6, atol=1e-7)
-    # stressed queries (x50, the reference's softcap stress) with cap 2: capped scores lie in [-2, 2],
-    # so every visible key's weight is within e^-4 of the max: output is a near-uniform average
-    Qs, Ks, Vs = normal_inputs(B, H, H, S, S, D, seed=10, q_mul=50.0)
-    ops = quantize_qkv(Qs, Ks, Vs)
-    pc = O.make_params(B, H, H, S, S, D, softcap=2.0)
-    o = O.attention(pc, *ops, block_n=32)
-    Vd = dequant_cols(ops[4], ops[5], O.FMT_E4M3)
-    assert np.all(np.abs(o) <= np.abs(Vd).max(axis=2, keepdims=True) + 1e-6)
+
+
+def _saturated_softcap_case(cap):
+    """Scores of exactly +-A (A = 32) after the softmax scale: Q row e0 * 16, K rows
+    +-16 e0 (powers of two, exact in E4M3), scale 1/8.  Keys k % 4 == 0 are '+', so
+    every 32-key P tile holds a '+' key and its amax is exactly 1.  V is 1.0 on '+'
+    keys and 3.0 on '-' keys (exact E4M3 after the along-keys quantization)."""
+    B, H, Sq, Sk, D = 1, 1, 4, 64, 64
+    Q = np.zeros((B, H, Sq, D), np.float32)
+    Q[..., 0] = 16.0
+    plus = (np.arange(Sk) % 4) == 0
+    K = np.zeros((B, H, Sk, D), np.float32)
+    K[0, 0, :, 0] = np.where(plus, 16.0, -16.0)
+    V = np.where(plus[:, None], 1.0, 3.0).astype(np.float32)[None, None].repeat(1, 0)
+    V = np.broadcast_to(V, (B, H, Sk, D)).copy()
+    ops = quantize_qkv(Q, K, V)
+    p = O.make_params(B, H, H, Sq, Sk, D, scale=0.125, softcap=cap)
+    return p, ops, int(plus.sum()), int((~plus).sum())
+
+
+def _e4m3_rne(y):
+    """Round a positive value in the E4M3 normal range to 3 mantissa bits, ties to even."""
+    e = np.floor(np.log2(y))
+    m = y / 2.0 ** e * 8.0
+    r = np.floor(m)
+    frac = m - r
+    r = r + (1.0 if frac > 0.5 or (frac == 0.5 and r % 2 == 1) else 0.0)
+    return r / 8.0 * 2.0 ** e
+
+
+@pytest.mark.parametrize("cap", [2.0, 3.0])
+def test_softcap_saturation_identity(cap):
+    """Gemma order (kernels/flash_attention_mx_gemma/flash_attention_model.py:263-267,
+    299-314): s <- cap * tanh((q.k) * scale / cap), then max and exp.  With scaled scores
+    +-32 the capped scores are +-cap*tanh(32/cap), so '+' keys weigh 1 and '-' keys
+    P = exp(-2 cap tanh(32/cap)); P sits in a tile of amax 1, so its R1 code is the E4M3
+    rounding of 256 P at scale 2^-8.  O = (n+ + 3 n- Pq) / (n+ + n- P) in every column.
+    Capping before the scale would give P = exp(-2 cap scale) and no cap at all P = 0."""
+    p, ops, npl, nmi = _saturated_softcap_case(cap)
+    o = O.attention(p, *ops, block_n=64)
+    P = float(np.float32(np.exp(-2.0 * cap * np.tanh(32.0 / cap))))
+    Pq = _e4m3_rne(256.0 * P) / 256.0
+    want = (npl + 3.0 * nmi * Pq) / (npl + nmi * P)
+    np.testing.assert_allclose(o, want, rtol=2e-7)
+    # the orders this test is meant to reject
+    P_swapped = float(np.float32(np.exp(-2.0 * cap * 0.125)))
+    Pq_swapped = _e4m3_rne(256.0 * P_swapped) / 256.0
+    swapped = (npl + 3.0 * nmi * Pq_swapped) / (npl + nmi * P_swapped)
+    assert abs(swapped - want) > 0.2 and abs(1.0 - want) > 1e-3
+    # and the oracle streaming over 32-key blocks gives the same (every tile has amax 1)
+    np.testing.assert_allclose(O.attention(p, *ops, block_n=32), want, rtol=2e-7)
+
+
+@pytest.mark.parametrize("cap", [2.0, 50.0])
+def test_softcap_closed_form_stressed_window(cap):
+    """The reference's softcap stress (Q x 50, kernels/flash_attention_mx_gemma/fa_gen_data.py:
+    77-79,98) under a causal sliding window, one key block: the oracle equals the dense
+    closed form scale -> cap*tanh(./cap) -> mask -> exp(S - max) -> R1 requant of P ->
+    PV / sum P.  With cap 2 every visible score lies in [-2, 2] (weights within e^-4 of the
+    max, far from the uncapped result); with cap 50 the stressed scores reach the
+    saturating part of tanh."""
+    B, H, S, D, W = 1, 1, 96, 64, 40
+    Q, K, V = normal_inputs(B, H, H, S, S, D, seed=31, q_mul=50.0)
+    ops = quantize_qkv(Q, K, V)
+    p = O.make_params(B, H, H, S, S, D, causal=True, window=W, softcap=cap)
+    o = O.attention(p, *ops, block_n=128)
+    qpos = np.arange(S)[:, None]
+    kpos = np.arange(S)[None, :]
+    mask = (kpos > qpos) | (kpos + W <= qpos)
+    want = _single_block_closed_form(*(a[0, 0] for a in ops), p.softmax_scale, mask, softcap=cap)
+    np.testing.assert_allclose(o[0, 0], want, rtol=1e-6, atol=1e-7)
+    uncapped = _single_block_closed_form(*(a[0, 0] for a in ops), p.softmax_scale, mask)
+    assert rel_l2(o[0, 0], uncapped) > (0.5 if cap == 2.0 else 1e-3)
+    if cap == 50.0:
+        # the stressed scores do reach the cap: some |scaled score| exceeds cap
+        Qd = dequant_rows(ops[0][0, 0], ops[1][0, 0], O.FMT_E4M3)
+        Kd = dequant_rows(ops[2][0, 0], ops[3][0, 0], O.FMT_E4M3)
+        assert np.abs(Qd @ Kd.T * p.softmax_scale).max() > cap
+
+
+def test_window_and_causal_edges_exact():
+    """Visible keys of row qpos are qpos - W + 1 .. qpos (the reference masks kpos + W <= qpos
+    and kpos > qpos, kernels/flash_attention_mx_gemma/flash_attention_model.py:288-296).
+    Perturbing the K row of each edge key tells visible from masked: keys qpos - W + 1 and
+    qpos change the row, keys qpos - W and qpos + 1 leave it bit-identical (K is blocked
+    along D, so one key's K row touches no other key's codes)."""
+    B, H, S, D, W = 1, 1, 128, 64, 40
+    Q, K, V = normal_inputs(B, H, H, S, S, D, seed=17)
+    p = O.make_params(B, H, H, S, S, D, causal=True, window=W)
+    base = O.attention(p, *quantize_qkv(Q, K, V), block_n=32)
+    rng = np.random.default_rng(18)
+    for qpos in (70, 100):
+        for key, visible in ((qpos - W + 1, True), (qpos, True), (qpos - W, False), (qpos + 1, False)):
+            K2 = K.copy()
+            K2[0, 0, key] = rng.standard_normal(D).astype(np.float32) * 3.0
+            o2 = O.attention(p, *quantize_qkv(Q, K2, V), block_n=32)
+            same = np.array_equal(base[0, 0, qpos], o2[0, 0, qpos])
+            assert same != visible, (qpos, key, visible)
 
 
 def test_split_kv_close_to_single_pass():
