@@ -29,6 +29,8 @@
  *   v   [B][Hkv][Sk][D]  v_sc [B][Hkv][Sk/32][D]    (32-blocks along the key axis,
  *                         the reference's V_scales[Sk/32][d], flash_attention_mx/gen_data.py:118-119)
  *   o   [B][Hq][Sq][D]   fp32
+ * With kv_stride = L > Sk (a KV cache of capacity L), k/v/k_sc/v_sc are laid out with L in
+ * place of Sk and only the first Sk keys of each (batch, KV head) are read.
  */
 #ifndef MXFA_H
 #define MXFA_H
@@ -40,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MXFA_VERSION 1
+#define MXFA_VERSION 2
 
 typedef enum {
   MXFA_OK = 0,
@@ -77,6 +79,9 @@ typedef struct {
   int32_t v_fmt;                            /* mxfa_fmt of V (Q and K are E4M3)                          */
   int32_t block_n;                          /* FA_BK: online-softmax key block; 0 = default (64)         */
   int32_t p_rule;                           /* mxfa_p_rule of P; 0 = MXFA_P_R1                           */
+  int32_t kv_stride;                        /* keys allocated per (batch, KV head) in k, k_sc, v, v_sc:   */
+                                            /* 0 = seq_k (dense); else >= seq_k, % 32 == 0 -- e.g. the    */
+                                            /* max_len of a KV cache (keys >= seq_k are never read)       */
 } mxfa_attn_params;
 
 /* ---- MX quantization (rule of lib/golden/mx_golden.cpp:146-190 with the element
@@ -146,8 +151,8 @@ typedef struct {
  * as 0.  After any sequence of appends (each starting at 0 or where the previous one
  * ended) the cache equals mxfa_quantize_rows / mxfa_quantize_cols of the whole sequence
  * (zero-padded to its 32-token block), bit for bit.  k_new, v_new: [B][Hkv][n_new][D] fp32.
- * Decode over L tokens: seq_k = L rounded up to 32, q_pos0 = L - 1 (the padding is masked
- * causally).  The reference has no cache (its operands are baked into a header); this is the
+ * Decode over L tokens straight from the cache: seq_k = L rounded up to 32, q_pos0 = L - 1
+ * (the padding is masked causally), kv_stride = max_len.  The reference has no cache (its operands are baked into a header); this is the
  * producer side of the decode path. */
 mxfa_status mxfa_kv_append(const mxfa_kv_params *p, const float *k_new, const float *v_new,
                            int32_t pos0, int32_t n_new, uint8_t *k_cache, uint8_t *k_sc,

@@ -14,6 +14,7 @@ struct FaArgs {
   float* part_o;      // decode: partial O  [B*Hq][nparts][D]
   float* part_ml;     // decode: partial (m, l) [B*Hq][nparts][2]
   int B, Hq, Hkv, Sq, Sk;
+  int Skc;            // keys allocated per (b, KV head) in k/ks/v/vs (>= Sk; base offsets use it)
   int q_pos0, window, causal, v_e3m2;
   int group;          // Hq / Hkv
   int hpw;            // prefill: query heads per workgroup

@@ -133,13 +133,15 @@ mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
   if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "v_fmt must be E4M3 or E3M2");
   if (p->block_n != 0 && p->block_n != 64) return fail(MXFA_ERR_UNSUPPORTED, "block_n must be 0 (default) or 64");
   if (p->p_rule != MXFA_P_R1 && p->p_rule != MXFA_P_R2) return fail(MXFA_ERR_INVALID_ARG, "p_rule must be R1 or R2");
+  if (p->kv_stride != 0 && (p->kv_stride < p->seq_k || p->kv_stride % 32))
+    return fail(MXFA_ERR_INVALID_ARG, "kv_stride must be 0 or a multiple of 32 that is >= seq_k");
   if (decode) {
     if (p->seq_q != 1) return fail(MXFA_ERR_INVALID_ARG, "decode needs seq_q == 1");
     if (p->num_q_heads / p->num_kv_heads > 32)
       return fail(MXFA_ERR_UNSUPPORTED, "decode supports at most 32 query heads per KV head");
   }
   int64_t qelems = (int64_t)p->batch * p->num_q_heads * p->seq_q * p->head_dim;
-  int64_t kelems = (int64_t)p->batch * p->num_kv_heads * p->seq_k * p->head_dim;
+  int64_t kelems = (int64_t)p->batch * p->num_kv_heads * (p->kv_stride ? p->kv_stride : p->seq_k) * p->head_dim;
   if (qelems > (int64_t)1 << 40 || kelems > (int64_t)1 << 40) return fail(MXFA_ERR_INVALID_ARG, "tensor too large");
   return MXFA_OK;
 }
@@ -158,6 +160,7 @@ FaArgs make_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* qs,
   std::memset(&a, 0, sizeof a);
   a.q = q; a.qs = qs; a.k = k; a.ks = ks; a.v = v; a.vs = vs; a.o = o;
   a.B = p->batch; a.Hq = p->num_q_heads; a.Hkv = p->num_kv_heads; a.Sq = p->seq_q; a.Sk = p->seq_k;
+  a.Skc = p->kv_stride ? p->kv_stride : p->seq_k;
   a.q_pos0 = p->q_pos0; a.window = p->window; a.causal = p->causal ? 1 : 0; a.v_e3m2 = p->v_fmt == MXFA_FMT_E3M2;
   a.group = p->num_q_heads / p->num_kv_heads;
   const float log2e = 1.4426950408889634f;

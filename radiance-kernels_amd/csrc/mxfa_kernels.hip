@@ -8,8 +8,9 @@
 // _gemma,_fp6,_stable}.  Per key block the reference runs QK^T on the MX mesh,
 // an online softmax + MX requant of P on the SIMT cores, then PV on the mesh and
 // a rescale of the O accumulator (kernels/flash_attention_mx_gqa/kernel.cpp:124-175,
-// flash_mx_impl.hpp:315-553).  Here both products run on scaled MFMA
-// (v_mfma_scale_f32_32x32x64_f8f6f4) and the softmax/requant on the VALU.
+// flash_mx_impl.hpp:315-553).  Here PV runs on the scaled MXFP8 MFMA
+// (v_mfma_scale_f32_32x32x64_f8f6f4), QK^T on the bf16 MFMA from an exact dequantization
+// of the MX operands (see "Precision" below), and the softmax/requant on the VALU.
 //
 // Scaled-MFMA operand layout (32x32x64, fp8), measured on gfx950:
 //   A (32 rows x 64 k): lane l holds row l%32; byte j of its 32 bytes is
@@ -839,10 +840,10 @@ __device__ void prefill_impl(const FaArgs& a) {
   const int wq_lo = a.q_pos0 + qw0, wq_hi = a.q_pos0 + min(qw0 + 31, a.Sq - 1);
   const bool wave_live = qw0 < a.Sq;
 
-  const uint8_t* kb = a.k + (int64_t)bk * a.Sk * D;
-  const uint8_t* ksb = a.ks + (int64_t)bk * a.Sk * (D / 32);
-  const uint8_t* vb = a.v + (int64_t)bk * a.Sk * D;
-  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Sk / 32) * D;
+  const uint8_t* kb = a.k + (int64_t)bk * a.Skc * D;
+  const uint8_t* ksb = a.ks + (int64_t)bk * a.Skc * (D / 32);
+  const uint8_t* vb = a.v + (int64_t)bk * a.Skc * D;
+  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Skc / 32) * D;
 
   WaveState<D> st;
 #pragma unroll
@@ -913,8 +914,10 @@ __device__ void prefill_impl(const FaArgs& a) {
   }
 }
 
-#define MXFA_PREFILL(D, SC, PR, NAME)                                                  \
-  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { prefill_impl<D, SC, PR>(a); }
+// Two workgroups per CU at D <= 128; D = 256 (about 470 registers per lane) fits one.
+template <int D> struct PrefillOcc { static constexpr int N = D == 256 ? 1 : 2; };
+#define MXFA_PREFILL(D, SC, PR, NAME)                                                                  \
+  extern "C" __global__ void __launch_bounds__(256, PrefillOcc<D>::N) NAME(FaArgs a) { prefill_impl<D, SC, PR>(a); }
 MXFA_PREFILL(64, false, P_R1, mxfa_prefill_d64)
 MXFA_PREFILL(128, false, P_R1, mxfa_prefill_d128)
 MXFA_PREFILL(256, false, P_R1, mxfa_prefill_d256)
@@ -977,10 +980,10 @@ __device__ void decode_split_impl(const FaArgs& a) {
   load_q_split<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
 
   // buffer resources end at Sk: rows past it read 0
-  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.k, (int64_t)bk * a.Sk * D, (int64_t)a.Sk * D);
-  const __amdgpu_buffer_rsrc_t rks = buf_rsrc(a.ks, (int64_t)bk * a.Sk * (D / 32), (int64_t)a.Sk * (D / 32));
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.v, (int64_t)bk * a.Sk * D, (int64_t)a.Sk * D);
-  const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(a.vs, (int64_t)bk * (a.Sk / 32) * D, (int64_t)(a.Sk / 32) * D);
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.k, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D);
+  const __amdgpu_buffer_rsrc_t rks = buf_rsrc(a.ks, (int64_t)bk * a.Skc * (D / 32), (int64_t)a.Sk * (D / 32));
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.v, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D);
+  const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(a.vs, (int64_t)bk * (a.Skc / 32) * D, (int64_t)(a.Sk / 32) * D);
 
   int klo, khi;
   key_limits(a, qpos, qvalid, klo, khi);
@@ -1207,10 +1210,10 @@ __device__ void decode_impl(const FaArgs& a) {
   v4i qb[D / 16];
   load_q<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
 
-  const uint8_t* kb = a.k + (int64_t)bk * a.Sk * D;
-  const uint8_t* ksb = a.ks + (int64_t)bk * a.Sk * (D / 32);
-  const uint8_t* vb = a.v + (int64_t)bk * a.Sk * D;
-  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Sk / 32) * D;
+  const uint8_t* kb = a.k + (int64_t)bk * a.Skc * D;
+  const uint8_t* ksb = a.ks + (int64_t)bk * a.Skc * (D / 32);
+  const uint8_t* vb = a.v + (int64_t)bk * a.Skc * D;
+  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Skc / 32) * D;
 
   // partial `part` of n_qblk takes the key blocks part, part + n_qblk, ...
   const int kend = a.Sk;

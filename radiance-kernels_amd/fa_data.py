@@ -66,10 +66,11 @@ def _u8(a):
 
 
 def export_fa_data(q, q_sc, k, k_sc, v, v_sc, *, block_n=64, q_pos0=0, layout="gqa", softcap=0.0, window=0,
-                   batch_index=0):
+                   batch_index=0, scale=None):
     """Our layouts (numpy uint8, batch dimension first) -> the reference arrays of one
     batch entry.  layout: "gqa" (causal), "gemma" (causal + softcap/window defines) or
-    "single" (one head, non-causal, all key blocks)."""
+    "single" (one head, non-causal, all key blocks).  scale: the softmax scale, written as
+    FA_SOFTMAX_SCALE_BF16 (bf16, as the reference's header holds it); default 1/sqrt(D)."""
     if layout not in LAYOUTS:
         raise ValueError(f"layout must be one of {LAYOUTS}")
     q, q_sc, k, k_sc, v, v_sc = (_u8(a)[batch_index] for a in (q, q_sc, k, k_sc, v, v_sc))
@@ -83,7 +84,7 @@ def export_fa_data(q, q_sc, k, k_sc, v, v_sc, *, block_n=64, q_pos0=0, layout="g
         raise ValueError("operand shapes do not match the library layouts")
     GK, GKB, Nblk = D // GROUP, Bk // GROUP, Sk // Bk
     d = dict(FA_SQ=Sq, FA_SK=Sk, FA_D=D, FA_GK=GK, FA_GKV=Sk // GROUP, FA_BK=Bk, FA_NBLK=Nblk, FA_GKB=GKB)
-    d["FA_SOFTMAX_SCALE_BF16"] = bf16_bits(1.0 / math.sqrt(D))
+    d["FA_SOFTMAX_SCALE_BF16"] = bf16_bits(1.0 / math.sqrt(D) if scale is None else scale)
     arr = {}
     if layout == "single":
         if NQ != 1 or NKV != 1:
@@ -117,13 +118,22 @@ def export_fa_data(q, q_sc, k, k_sc, v, v_sc, *, block_n=64, q_pos0=0, layout="g
     return FaData(layout, d, arr)
 
 
-def import_fa_data(fd):
+def import_fa_data(fd, scale="header"):
     """Reference arrays -> (q, q_sc, k, k_sc, v, v_sc) in our layouts (batch 1) and the
-    keyword arguments of mxfa.make_params for the same attention."""
+    keyword arguments of mxfa.make_params for the same attention.  scale: "header" takes
+    the softmax scale the reference device kernels compute with, the bf16
+    FA_SOFTMAX_SCALE_BF16 (kernels/flash_attention_mx_gqa/kernel.cpp:52,149; 1/sqrt(128)
+    is 0.08837890625 there); "fp32" takes 1/sqrt(D) as the reference's Python model does."""
     d, a = fd.defines, fd.arrays
     Sq, Sk, D, Bk = d["FA_SQ"], d["FA_SK"], d["FA_D"], d["FA_BK"]
     GK, GKB = D // GROUP, Bk // GROUP
-    params = dict(B=1, Sq=Sq, Sk=Sk, D=D, scale=1.0 / math.sqrt(D), block_n=Bk)
+    if scale == "header" and "FA_SOFTMAX_SCALE_BF16" in d:
+        sc = float(np.array([d["FA_SOFTMAX_SCALE_BF16"] << 16], np.uint32).view(np.float32)[0])
+    elif scale in ("header", "fp32"):
+        sc = 1.0 / math.sqrt(D)
+    else:
+        raise ValueError('scale must be "header" or "fp32"')
+    params = dict(B=1, Sq=Sq, Sk=Sk, D=D, scale=sc, block_n=Bk)
     if fd.layout == "single":
         q = a["QK_A_in"].reshape(1, 1, Sq, D)
         q_sc = np.ascontiguousarray(a["QK_A_scales_row"].T).reshape(1, 1, Sq, GK)

@@ -48,15 +48,44 @@ class AttnParams(ctypes.Structure):
         ("seq_q", ctypes.c_int32), ("seq_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("causal", ctypes.c_int32), ("q_pos0", ctypes.c_int32), ("window", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("v_fmt", ctypes.c_int32),
-        ("block_n", ctypes.c_int32), ("p_rule", ctypes.c_int32),
+        ("block_n", ctypes.c_int32), ("p_rule", ctypes.c_int32), ("kv_stride", ctypes.c_int32),
     ]
 
 
 def make_params(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, scale=None, softcap=0.0,
-                v_fmt=FMT_E4M3, block_n=0, p_rule=P_R1):
+                v_fmt=FMT_E4M3, block_n=0, p_rule=P_R1, kv_stride=0):
     return AttnParams(B, Hq, Hkv, Sq, Sk, D, int(bool(causal)), int(q_pos0), int(window),
                       float(scale if scale is not None else 1.0 / math.sqrt(D)), float(softcap), int(v_fmt),
-                      int(block_n), int(p_rule))
+                      int(block_n), int(p_rule), int(kv_stride))
+
+
+def _need(t, dtype, shape, name):
+    """Device, dtype, layout and shape check of one operand before its pointer is passed
+    on (the kernels read through raw pointers: a host, short or strided tensor would be
+    read out of bounds)."""
+    import torch
+    if not (isinstance(t, torch.Tensor) and t.is_cuda):
+        raise MxfaError(1, f"{name} must be a CUDA tensor")
+    if t.dtype != dtype:
+        raise MxfaError(1, f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise MxfaError(1, f"{name} must be contiguous")
+    if tuple(t.shape) != tuple(shape):
+        raise MxfaError(1, f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+def _check_attn_operands(p, q, qs, k, ks, v, vs, out):
+    import torch
+    B, Hq, Hkv, Sq, D = p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.head_dim
+    L = p.kv_stride or p.seq_k
+    u8 = torch.uint8
+    _need(q, u8, (B, Hq, Sq, D), "q")
+    _need(qs, u8, (B, Hq, Sq, D // 32), "q_sc")
+    _need(k, u8, (B, Hkv, L, D), "k")
+    _need(ks, u8, (B, Hkv, L, D // 32), "k_sc")
+    _need(v, u8, (B, Hkv, L, D), "v")
+    _need(vs, u8, (B, Hkv, L // 32, D), "v_sc")
+    _need(out, torch.float32, (B, Hq, Sq, D), "out")
 
 
 class KvParams(ctypes.Structure):
@@ -215,9 +244,12 @@ def fill_normal(x, seed, outlier_p=0.0, outlier_mul=20.0, stream=None):
 
 
 def prefill(p, q, qs, k, ks, v, vs, out=None, stream=None):
+    """O [B, Hq, Sq, D] fp32 of MXFP8 attention (mxfa_prefill); operands in the C-ABI layouts
+    (k/v/k_sc/v_sc with p.kv_stride keys per (batch, KV head) when it is set)."""
     import torch
     if out is None:
         out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device=q.device)
+    _check_attn_operands(p, q, qs, k, ks, v, vs, out)
     _check(lib().mxfa_prefill(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
                               _stream(stream)))
     return out
@@ -239,6 +271,8 @@ def decode(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     if out is None:
         out = torch.empty((p.batch, p.num_q_heads, 1, p.head_dim), dtype=torch.float32, device=q.device)
+    _check_attn_operands(p, q, qs, k, ks, v, vs, out)
+    _need(workspace, torch.uint8, (workspace.numel(),), "workspace")
     _check(lib().mxfa_decode(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
                              _ptr(workspace), workspace.numel(), _stream(stream)))
     return out
@@ -259,12 +293,24 @@ class KvCache:
         self.tail = torch.zeros((B, H, 32, D), dtype=torch.float32, device=device)
         self.length = 0
 
+    def decode_params(self, Hq, **kw):
+        """mxfa_attn_params for decoding the next query over the cache as it stands: seq_k =
+        length rounded up to 32, q_pos0 = length - 1 (the padding is masked causally),
+        kv_stride = max_len (decode reads the cache tensors in place)."""
+        P = self.params
+        sk = (self.length + 31) // 32 * 32
+        return make_params(P.batch, Hq, P.num_kv_heads, 1, sk, P.head_dim, causal=True, q_pos0=self.length - 1,
+                           v_fmt=P.v_fmt, kv_stride=P.max_len, **kw)
+
     def append(self, k_new, v_new, stream=None):
         """k_new, v_new: contiguous float32 [B, Hkv, n_new, D] CUDA tensors."""
         import torch
-        for t in (k_new, v_new):
-            assert t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.dim() == 4
-        n = k_new.shape[2]
+        P = self.params
+        n = k_new.shape[2] if k_new.dim() == 4 else -1
+        _need(k_new, torch.float32, (P.batch, P.num_kv_heads, n, P.head_dim), "k_new")
+        _need(v_new, torch.float32, (P.batch, P.num_kv_heads, n, P.head_dim), "v_new")
+        if self.length + n > P.max_len:
+            raise MxfaError(1, f"append of {n} tokens at {self.length} exceeds max_len {P.max_len}")
         _check(lib().mxfa_kv_append(ctypes.byref(self.params), _ptr(k_new), _ptr(v_new), self.length, n,
                                     _ptr(self.k), _ptr(self.ks), _ptr(self.v), _ptr(self.vs), _ptr(self.tail),
                                     _stream(stream)))

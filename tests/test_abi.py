@@ -38,7 +38,7 @@ def test_code_object_present_and_for_gfx950():
 
 def test_version_and_status_strings():
     L = mxfa.lib()
-    assert L.mxfa_version() == 1
+    assert L.mxfa_version() == 2
     assert L.mxfa_status_string(0) == b"ok"
     assert L.mxfa_status_string(5) == b"workspace too small"
 
@@ -61,12 +61,14 @@ def _call_prefill(p):
     (dict(block_n=128), 2),
     (dict(p_rule=2), 1),
     (dict(p_rule=-1), 1),
+    (dict(kv_stride=32), 1),             # below seq_k
+    (dict(kv_stride=100), 1),            # not a multiple of 32
 ])
 def test_prefill_argument_validation(kw, status):
-    a = dict(B=1, Hq=2, Hkv=2, Sq=32, Sk=64, D=64, window=0, softcap=0.0, block_n=0, p_rule=0)
+    a = dict(B=1, Hq=2, Hkv=2, Sq=32, Sk=64, D=64, window=0, softcap=0.0, block_n=0, p_rule=0, kv_stride=0)
     a.update(kw)
     p = mxfa.make_params(a["B"], a["Hq"], a["Hkv"], a["Sq"], a["Sk"], a["D"], window=a["window"],
-                         softcap=a["softcap"], block_n=a["block_n"], p_rule=a["p_rule"])
+                         softcap=a["softcap"], block_n=a["block_n"], p_rule=a["p_rule"], kv_stride=a["kv_stride"])
     assert _call_prefill(p) == status
     assert mxfa.lib().mxfa_last_error()
 

@@ -171,3 +171,22 @@ def test_export_rejects_bad_shapes():
         F.export_fa_data(*ops, softcap=30.0)                 # softcap needs the gemma layout
     with pytest.raises(ValueError):
         F.read_header("#define FA_SQ 2\n#define FA_D 2\nstatic const uint8_t QK_A_in[FA_SQ][FA_D] = { {0x1, 0x2} };")
+
+
+def test_softmax_scale_header_and_fp32():
+    """The reference's device kernels compute with the header's bf16 softmax scale
+    (kernels/flash_attention_mx_gqa/kernel.cpp:52,149): at D = 128 that is 0.08837890625,
+    not 1/sqrt(128).  import_fa_data takes it by default and 1/sqrt(D) on request; export
+    writes a caller's scale."""
+    ops = _operands(4, 2, 32, 128, 128, seed=6)
+    fd = F.read_header(F.header_text(F.export_fa_data(*ops, block_n=64, q_pos0=96)))
+    assert fd.defines["FA_SOFTMAX_SCALE_BF16"] == 0x3DB5
+    _, prm = F.import_fa_data(fd)
+    assert prm["scale"] == 0.08837890625
+    _, prm = F.import_fa_data(fd, scale="fp32")
+    assert prm["scale"] == np.float32(1.0 / np.sqrt(128.0)) or abs(prm["scale"] - 1.0 / np.sqrt(128.0)) < 1e-12
+    fd = F.read_header(F.header_text(F.export_fa_data(*ops, block_n=64, q_pos0=96, scale=0.0625)))
+    assert fd.defines["FA_SOFTMAX_SCALE_BF16"] == 0x3D80
+    assert F.import_fa_data(fd)[1]["scale"] == 0.0625
+    with pytest.raises(ValueError):
+        F.import_fa_data(fd, scale="other")

@@ -108,6 +108,14 @@ def test_baseline_configs_sampled_heads(cfg):
                  heads=[3], check_codes=False)
 
 
+def test_softcap_stress_config4_shape():
+    """The reference's softcap stress (Q x 50, kernels/flash_attention_mx_gemma/fa_gen_data.py:
+    77-79,98) at the Gemma config's full shape: B=1 Hq=16 Hkv=8 S=8192 D=256, window 4096,
+    softcap 50, E3M2 V; sampled heads against the oracle."""
+    run_case(1, 16, 8, 8192, 8192, 256, causal=True, window=4096, softcap=50.0, v_fmt=mxfa.FMT_E3M2, seed=24,
+             q_mul=50.0, heads=[6], check_codes=False)
+
+
 def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=0.0, p_rule=mxfa.P_R1):
     print(f"decode B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} seed {seed} p_rule {p_rule}", flush=True)
     fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L, D, seed, v_fmt=v_fmt)
@@ -133,6 +141,13 @@ def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=
 
 def test_decode_small():
     run_decode(4, 32, 8, 1024, 128, seed=30)
+
+
+def test_decode_group_32():
+    """32 query heads per KV head, the largest group decode takes: all 32 score columns
+    are valid and the partials merge in the combine kernel."""
+    run_decode(2, 32, 1, 1024, 128, seed=34)
+    run_decode(1, 64, 2, 640, 64, seed=35)
 
 
 def test_decode_ragged_and_e3m2():

@@ -105,3 +105,30 @@ def test_gemm_deterministic():
     c2 = mxfa.gemm(*dev)
     torch.cuda.synchronize()
     assert torch.equal(c1, c2)
+
+
+def test_gemm_benched_shape_sampled():
+    """The shape the bench quotes (QKV projection of configs[2]: M 8192, N 6144, K 4096):
+    the whole C is computed and checked finite; 96 sampled rows x 96 sampled columns
+    (every tile row and column of the 256 x 256 C tiles, and tile edges) against the
+    oracle's exact sums, to the same bounds."""
+    M, N, K = 8192, 6144, 4096
+    print(f"gemm benched shape M{M} N{N} K{K}", flush=True)
+    rng = np.random.default_rng(77)
+    a, b = _codes(rng, (M, K), mxfa.FMT_E4M3), _codes(rng, (K, N), mxfa.FMT_E4M3)
+    sa = rng.integers(112, 142, (K // 32, M)).astype(np.uint8)
+    sb = rng.integers(112, 142, (K // 32, N)).astype(np.uint8)
+    dev = [torch.from_numpy(x).to(DEV) for x in (a, sa, b, sb)]
+    out = mxfa.gemm(dev[0], dev[1], dev[2], dev[3])
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "coverage"
+    rows = np.unique(np.concatenate([np.arange(0, M, 256), np.arange(255, M, 256)[:32], rng.integers(0, M, 32)]))[:96]
+    cols = np.unique(np.concatenate([np.arange(0, N, 256), np.arange(255, N, 256)[:24], rng.integers(0, N, 48)]))[:96]
+    c = np_(out)[np.ix_(rows, cols)].astype(np.float64)
+    want, ab = O.mx_gemm(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[:, rows]),
+                         np.ascontiguousarray(b[:, cols]), np.ascontiguousarray(sb[:, cols]),
+                         mxfa.FMT_E4M3, mxfa.FMT_E4M3, with_abs=True)
+    err = np.abs(c - want)
+    print(f"   sampled rel-L2 {rel_l2(c, want):.2e}, max err / sum|terms| {float((err / ab).max()):.2e}", flush=True)
+    assert np.all(err <= ab * 2.0 ** -8 + 1e-38)
+    assert rel_l2(c, want) <= 1e-3

@@ -84,3 +84,40 @@ def test_decode_over_appended_cache():
     rel, mab = errors(np_(o), want)
     print(f"   decode over appended cache: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
     assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+
+
+def test_decode_in_place_on_cache_with_capacity():
+    """Decode reads the cache tensors in place (kv_stride = max_len > seq_k) for several
+    (batch, KV head) pairs: the same O, bit for bit, as decoding contiguous copies of the
+    first seq_k keys, and within tolerance of the oracle."""
+    B, Hq, Hkv, D, Lcap, n = 3, 16, 4, 128, 1024, 333
+    rng = np.random.default_rng(420)
+    cache = mxfa.KvCache(B, Hkv, D, Lcap)
+    Kd = torch.from_numpy(rng.standard_normal((B, Hkv, n, D)).astype(np.float32)).to(DEV)
+    Vd = torch.from_numpy(rng.standard_normal((B, Hkv, n, D)).astype(np.float32)).to(DEV)
+    cache.append(Kd[:, :, :200].contiguous(), Vd[:, :, :200].contiguous())
+    cache.append(Kd[:, :, 200:].contiguous(), Vd[:, :, 200:].contiguous())
+    Q = torch.empty((B, Hq, 1, D), dtype=torch.float32, device=DEV)
+    mxfa.fill_normal(Q, 421)
+    q, qs = mxfa.quantize_rows(Q)
+    p = cache.decode_params(Hq)
+    assert p.kv_stride == Lcap and p.seq_k == 352 and p.q_pos0 == n - 1
+    got = mxfa.decode(p, q, qs, cache.k, cache.ks, cache.v, cache.vs)
+    sk = p.seq_k
+    k, ks = cache.k[:, :, :sk].contiguous(), cache.ks[:, :, :sk].contiguous()
+    v, vs = cache.v[:, :, :sk].contiguous(), cache.vs[:, :, :sk // 32].contiguous()
+    pc = mxfa.make_params(B, Hq, Hkv, 1, sk, D, causal=True, q_pos0=n - 1)
+    dense = mxfa.decode(pc, q, qs, k, ks, v, vs)
+    # prefill over the cache in place (one query row per head at the last position)
+    pp = mxfa.make_params(B, Hq, Hkv, 1, sk, D, causal=True, q_pos0=n - 1, kv_stride=Lcap)
+    pre_inplace = mxfa.prefill(pp, q, qs, cache.k, cache.ks, cache.v, cache.vs)
+    pre_dense = mxfa.prefill(pc, q, qs, k, ks, v, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(got, dense)
+    assert torch.equal(pre_inplace, pre_dense)
+    n_parts, _ = mxfa.decode_plan(pc)
+    want = O.attention(oracle_params(pc), np_(q), np_(qs), np_(k), np_(ks), np_(v), np_(vs),
+                       block_n=mxfa.DEFAULT_BLOCK_N, n_parts=n_parts)
+    rel, mab = errors(np_(got), want)
+    print(f"   in-place decode: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
