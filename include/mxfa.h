@@ -131,6 +131,22 @@ mxfa_status mxfa_decode(const mxfa_attn_params *p,
                         const uint8_t *v_cache, const uint8_t *v_sc,
                         float *o, void *workspace, size_t workspace_bytes, void *stream);
 
+/* mxfa_decode without a workspace and without any allocation, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  No counterpart in the reference (it has no decode kernel and allocates
+ * nothing at all).  The partials live in a device array inside the code object
+ * (MXFA_DECODE_SCRATCH_BYTES = 16 MiB per device, held until the process ends); shapes whose
+ * partials need more (mxfa_decode_plan's workspace_bytes) are rejected with
+ * MXFA_ERR_WORKSPACE before any launch.  The code object must already be loaded on the
+ * current device (mxfa_init(), or any earlier call there): otherwise MXFA_ERR_MODULE, since
+ * loading it would allocate.  Same O as mxfa_decode, bit for bit.  Calls that overlap on
+ * one device share the array and race: order them on one stream. */
+mxfa_status mxfa_decode_noalloc(const mxfa_attn_params *p,
+                                const uint8_t *q, const uint8_t *q_sc,
+                                const uint8_t *k_cache, const uint8_t *k_sc,
+                                const uint8_t *v_cache, const uint8_t *v_sc,
+                                float *o, void *stream);
+
 /* ---- KV cache ---- */
 
 /* KV-cache shape for mxfa_kv_append: caches k [B][Hkv][max_len][D] + k_sc [B][Hkv][max_len][D/32],

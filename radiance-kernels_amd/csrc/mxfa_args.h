@@ -27,6 +27,10 @@ struct FaArgs {
   float cap_log2;     // softcap * log2(e) (0 = no softcap)
 };
 
+// Size of the code object's device-resident decode scratch (mxfa_decode_scratch), the partials
+// of mxfa_decode_noalloc: B * Hq * n_parts * (D + 2) floats at most.
+#define MXFA_DECODE_SCRATCH_BYTES (16u << 20)
+
 // MX GEMM kernel arguments: C [M][N] fp32 = A [M][K] x B [K][N] (element codes) with E8M0
 // scales SA [K/32][M] and SB [K/32][N].
 struct GemmArgs {

@@ -53,6 +53,8 @@ constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 struct DeviceModule {
   hipModule_t mod = nullptr;
   hipFunction_t fn[kNumKernels] = {};
+  void* decode_scratch = nullptr;     // this device's address of mxfa_decode_scratch
+  size_t decode_scratch_bytes = 0;
 };
 
 std::mutex g_mu;
@@ -95,8 +97,32 @@ mxfa_status module_for_current(DeviceModule** out) {
       return fail(MXFA_ERR_MODULE, std::string("kernel ") + kKernelNames[i] + " missing from " + path);
     }
   }
+  // The device address of the decode scratch array in this device's copy of the module (the
+  // module-API form of hipGetSymbolAddress): taken here, with the device current, and only
+  // this address is ever passed to a kernel.
+  hipDeviceptr_t sp = nullptr;
+  e = hipModuleGetGlobal(&sp, &dm.decode_scratch_bytes, dm.mod, "mxfa_decode_scratch");
+  if (e != hipSuccess || !sp || dm.decode_scratch_bytes < MXFA_DECODE_SCRATCH_BYTES) {
+    (void)hipModuleUnload(dm.mod);
+    return fail(MXFA_ERR_MODULE, std::string("hipModuleGetGlobal(mxfa_decode_scratch) in ") + path + ": " +
+                                     (e != hipSuccess ? hipGetErrorString(e) : "missing or too small"));
+  }
+  dm.decode_scratch = reinterpret_cast<void*>(sp);
   auto res = g_mods.emplace(dev, dm);
   *out = &res.first->second;
+  return MXFA_OK;
+}
+
+// Module of the current device if it is already loaded (never loads: no allocation).
+mxfa_status loaded_module_for_current(DeviceModule** out) {
+  int dev = -1;
+  MXFA_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_mods.find(dev);
+  if (it == g_mods.end())
+    return fail(MXFA_ERR_MODULE, "no code object loaded on device " + std::to_string(dev) +
+                                     ": call mxfa_init() on it before mxfa_decode_noalloc");
+  *out = &it->second;
   return MXFA_OK;
 }
 
@@ -421,20 +447,15 @@ mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* n_parts, size_t
   return MXFA_OK;
 }
 
-mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k_cache,
-                        const uint8_t* k_sc, const uint8_t* v_cache, const uint8_t* v_sc, float* o, void* workspace,
-                        size_t workspace_bytes, void* stream) {
-  if (mxfa_status st = check_params(p, true)) return st;
-  const void* ptrs[] = {q, q_sc, k_cache, k_sc, v_cache, v_sc, o};
-  if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
-  size_t need = 0;
-  int32_t sl = 0;
-  mxfa_decode_plan(p, &sl, &need);
-  if (!workspace || workspace_bytes < need)
-    return fail(MXFA_ERR_WORKSPACE, "decode workspace must be at least " + std::to_string(need) + " bytes");
-  if (!aligned16(workspace)) return fail(MXFA_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
-  DeviceModule* dm;
-  if (mxfa_status st = module_for_current(&dm)) return st;
+}  // extern "C"
+
+namespace {
+
+// The decode launches of mxfa_decode and mxfa_decode_noalloc (arguments already checked;
+// workspace holds the partials of the two-launch path).
+mxfa_status decode_launch(DeviceModule* dm, const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc,
+                          const uint8_t* k_cache, const uint8_t* k_sc, const uint8_t* v_cache, const uint8_t* v_sc,
+                          float* o, void* workspace, void* stream) {
   FaArgs a = make_args(p, q, q_sc, k_cache, k_sc, v_cache, v_sc, o);
   const int nparts = decode_parts(p);
   a.n_qblk = nparts;
@@ -460,6 +481,45 @@ mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8
     return st;
   if (a.fuse_combine) return MXFA_OK;
   return launch(dm, "mxfa_decode_combine", dim3((unsigned)nbh), dim3((unsigned)p->head_dim), args, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+mxfa_status mxfa_decode(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k_cache,
+                        const uint8_t* k_sc, const uint8_t* v_cache, const uint8_t* v_sc, float* o, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (mxfa_status st = check_params(p, true)) return st;
+  const void* ptrs[] = {q, q_sc, k_cache, k_sc, v_cache, v_sc, o};
+  if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
+  size_t need = 0;
+  int32_t sl = 0;
+  mxfa_decode_plan(p, &sl, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(MXFA_ERR_WORKSPACE, "decode workspace must be at least " + std::to_string(need) + " bytes");
+  if (!aligned16(workspace)) return fail(MXFA_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  return decode_launch(dm, p, q, q_sc, k_cache, k_sc, v_cache, v_sc, o, workspace, stream);
+}
+
+mxfa_status mxfa_decode_noalloc(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc,
+                                const uint8_t* k_cache, const uint8_t* k_sc, const uint8_t* v_cache,
+                                const uint8_t* v_sc, float* o, void* stream) {
+  if (mxfa_status st = check_params(p, true)) return st;
+  const void* ptrs[] = {q, q_sc, k_cache, k_sc, v_cache, v_sc, o};
+  if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
+  size_t need = 0;
+  int32_t sl = 0;
+  mxfa_decode_plan(p, &sl, &need);
+  if (need > MXFA_DECODE_SCRATCH_BYTES)
+    return fail(MXFA_ERR_WORKSPACE, "mxfa_decode_noalloc: the partials of this shape need " + std::to_string(need) +
+                                        " bytes, above the " + std::to_string(MXFA_DECODE_SCRATCH_BYTES) +
+                                        "-byte device scratch; use mxfa_decode with a workspace");
+  DeviceModule* dm;
+  if (mxfa_status st = loaded_module_for_current(&dm)) return st;
+  return decode_launch(dm, p, q, q_sc, k_cache, k_sc, v_cache, v_sc, o, dm->decode_scratch, stream);
 }
 
 }  // extern "C"

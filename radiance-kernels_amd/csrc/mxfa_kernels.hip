@@ -1287,6 +1287,14 @@ __device__ void decode_impl(const FaArgs& a) {
   }
 }
 
+// Decode partials of mxfa_decode_noalloc: one array per device, in this code object, so that
+// callers that cannot allocate (graph capture, serving loops) need no workspace.  The host
+// takes its device address from the loaded module (hipModuleGetGlobal) once per device and
+// passes that address to the kernels as part_o / part_ml, like a caller's workspace; the
+// partials of a call are written before they are read, so nothing needs clearing, and calls
+// that overlap on one device share (and race on) the array.
+__device__ __attribute__((used, aligned(256))) uint8_t mxfa_decode_scratch[MXFA_DECODE_SCRATCH_BYTES];
+
 #define MXFA_DECODE_SPLIT(D, SC, PR, NAME)                                             \
   extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC, PR>(a); }
 #define MXFA_DECODE(D, SC, PR, NAME)                                                   \

@@ -102,6 +102,7 @@ class GemmParams(ctypes.Structure):
 
 
 EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
+           "mxfa_decode_noalloc",
            "mxfa_kv_append", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
            "mxfa_last_error", "mxfa_version", "mxfa_gemm")
 
@@ -123,6 +124,7 @@ def lib():
         L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
         L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
         L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
+        L.mxfa_decode_noalloc.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
         L.mxfa_softmax_requant.argtypes = [f32p, f32p, ctypes.c_float, ctypes.c_int64, ctypes.c_int32,
                                            ctypes.c_int32, f32p, u8p, u8p, f32p, vp]
         L.mxfa_fill_normal.argtypes = [f32p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp]
@@ -133,7 +135,7 @@ def lib():
         L.mxfa_last_error.restype = ctypes.c_char_p
         L.mxfa_version.restype = ctypes.c_int32
         for name in ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
-                     "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_kv_append", "mxfa_gemm"):
+                     "mxfa_decode_noalloc", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_kv_append", "mxfa_gemm"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -275,6 +277,18 @@ def decode(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):
     _need(workspace, torch.uint8, (workspace.numel(),), "workspace")
     _check(lib().mxfa_decode(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
                              _ptr(workspace), workspace.numel(), _stream(stream)))
+    return out
+
+
+DECODE_SCRATCH_BYTES = 16 << 20        # MXFA_DECODE_SCRATCH_BYTES
+
+
+def decode_noalloc(p, q, qs, k, ks, v, vs, out, stream=None):
+    """mxfa_decode_noalloc: decode with the partials in the library's per-device scratch
+    (no workspace, nothing allocated by the call; out must be given)."""
+    _check_attn_operands(p, q, qs, k, ks, v, vs, out)
+    _check(lib().mxfa_decode_noalloc(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs),
+                                     _ptr(out), _stream(stream)))
     return out
 
 

@@ -32,7 +32,7 @@ def test_code_object_present_and_for_gfx950():
     assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     assert b"gfx950" in data
     for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows",
-              "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2"):
+              "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2", "mxfa_decode_scratch"):
         assert k.encode() in data
 
 
@@ -145,3 +145,20 @@ def test_gemm_argument_validation():
     ok = G(64, 64, 64, 0, 0)
     assert L.mxfa_gemm(ctypes.byref(ok), None, ptr, ptr, ptr, ptr, None) == 1
     assert L.mxfa_gemm(None, ptr, ptr, ptr, ptr, ptr, None) == 1
+
+
+def test_decode_noalloc_rejects_before_touching_the_device():
+    """mxfa_decode_noalloc checks its arguments and the size of the partials against the
+    16 MiB device scratch before any HIP call: an oversized shape is MXFA_ERR_WORKSPACE
+    (the status is the same on a host without a GPU), NULL pointers MXFA_ERR_INVALID_ARG."""
+    L = mxfa.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    ptr = ctypes.c_void_p(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16)
+    big = mxfa.make_params(512, 64, 2, 1, 4096, 256, causal=True, q_pos0=4095)
+    _, ws = mxfa.decode_plan(big)
+    assert ws > mxfa.DECODE_SCRATCH_BYTES
+    assert L.mxfa_decode_noalloc(ctypes.byref(big), ptr, ptr, ptr, ptr, ptr, ptr, ptr, None) == 5
+    assert b"16777216-byte device scratch" in L.mxfa_last_error()
+    ok = mxfa.make_params(64, 32, 8, 1, 8192, 128, causal=True, q_pos0=8191)
+    assert mxfa.decode_plan(ok)[1] <= mxfa.DECODE_SCRATCH_BYTES
+    assert L.mxfa_decode_noalloc(ctypes.byref(ok), None, None, None, None, None, None, None, None) == 1
