@@ -15,7 +15,7 @@
  *
  * Conventions
  *  - All tensors are caller-owned device memory; the library allocates nothing per
- *    call (decode takes a caller workspace).  Element codes are one byte each
+ *    call (mxfa_prefill_ws and mxfa_decode take a caller workspace).  Element codes are one byte each
  *    (E3M2 codes in the low 6 bits).  Base pointers must be 16-byte aligned.
  *  - Calls are asynchronous on `stream` (a hipStream_t; NULL = default stream) and
  *    never synchronize the host.  Results are deterministic (fixed reduction order,
@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MXFA_VERSION 2
+#define MXFA_VERSION 3
 
 typedef enum {
   MXFA_OK = 0,
@@ -50,7 +50,7 @@ typedef enum {
   MXFA_ERR_UNSUPPORTED = 2,   /* valid but not implemented (e.g. head_dim 96) */
   MXFA_ERR_HIP = 3,           /* a HIP runtime call failed */
   MXFA_ERR_MODULE = 4,        /* the gfx950 code object could not be loaded */
-  MXFA_ERR_WORKSPACE = 5      /* decode workspace missing or too small */
+  MXFA_ERR_WORKSPACE = 5      /* workspace missing or too small */
 } mxfa_status;
 
 typedef enum { MXFA_FMT_E4M3 = 0, MXFA_FMT_E3M2 = 1 } mxfa_fmt;
@@ -117,6 +117,25 @@ mxfa_status mxfa_prefill(const mxfa_attn_params *p,
                          const uint8_t *k, const uint8_t *k_sc,
                          const uint8_t *v, const uint8_t *v_sc,
                          float *o, void *stream);
+
+/* Prefill with a caller workspace: the faster path for head_dim <= 128 with E4M3 V.  A first
+ * launch writes the bf16 value of every K element (E4M3 code x 2^(scale - 127), exact in bf16)
+ * into the workspace; the attention kernel then streams that copy and V into LDS by DMA and
+ * runs three waves per SIMD.  Same inputs, outputs and O as mxfa_prefill (within the same
+ * tolerance of the reference's algorithm; the two kernels order no sum differently, but the
+ * bf16 K operand is exact in both).  *workspace_bytes = batch * num_kv_heads * seq_k *
+ * head_dim * 2 for those shapes, 0 for the others (then mxfa_prefill_ws runs mxfa_prefill and
+ * ignores the workspace).  A workspace smaller than the plan is MXFA_ERR_WORKSPACE.
+ * Replaces the same reference entry point as mxfa_prefill (kernels/flash_attention_mx_gqa/
+ * kernel.cpp:91-191); the reference's matrix unit takes K's codes and scales as they are, so
+ * it has no such copy: the workspace is this library's operand layout for the bf16 score MFMA. */
+mxfa_status mxfa_prefill_plan(const mxfa_attn_params *p, size_t *workspace_bytes);
+
+mxfa_status mxfa_prefill_ws(const mxfa_attn_params *p,
+                            const uint8_t *q, const uint8_t *q_sc,
+                            const uint8_t *k, const uint8_t *k_sc,
+                            const uint8_t *v, const uint8_t *v_sc,
+                            float *o, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Split-KV decode plan for seq_q == 1 (q_pos0 is the query's position, normally
  * seq_k - 1): the 64-key blocks are dealt to *n_parts independent partials (partial i

@@ -72,6 +72,21 @@ __device__ __forceinline__ uint32_t scale_code_p_fast(float amax) {
   return sc;
 }
 
+// The same code without a branch, for a tile amax in [0, 1] (every P tile: amax =
+// exp2((tile max - row max) * c) with tile max <= row max).  floorf(log2f(amax)) is e + 1
+// instead of e when the mantissa lies within delta of 2^23, where delta depends on the
+// binade's distance below 2^0, u = 126 - E: delta = 0x2C >> (6 - floor(log2 u)) for
+// u >= 2 (the 0x01, 0x02, 0x05, 0x0B, 0x16, 0x2C of scale_code_p) and 0 below.  Adding
+// delta to the bit pattern carries into the exponent field exactly when the mantissa
+// reaches 2^23 - delta, so the code is max(((bits + delta) >> 23) - 8, 0).  Equal to
+// scale_code_p for every float in [0, 1] (checked exhaustively).
+__device__ __forceinline__ uint32_t scale_code_p_nb(float amax) {
+  const uint32_t b = __float_as_uint(amax);
+  const uint32_t u = __builtin_elementwise_sub_sat(126u, b >> 23);   // 126 - E, 0 at E = 127
+  const uint32_t delta = 0x58000000u >> __builtin_clz(u | 1u);
+  return __builtin_elementwise_sub_sat((b + delta) >> 23, 8u);
+}
+
 // Rule R4, the reference's SIMT block quantizer (kernels/simt_quant/kernel.cpp:43-117):
 // E4M3 code of y with round-half-even, saturation at 448 and subnormals kept (2^-9 grid).
 __device__ __forceinline__ uint32_t r4_round_shift(uint32_t v, int sh) {   // RNE of v / 2^sh, sh > 0
@@ -222,7 +237,7 @@ __device__ __forceinline__ uint32_t cvt_pack4_in_place(float y0, float y1, float
 __device__ __forceinline__ uint32_t p_pack4(float p0, float p1, float p2, float p3, const PTileBounds& b) {
   const uint32_t w = cvt_pack4_in_place(p_flush(p0, b), p_flush(p1, b), p_flush(p2, b), p_flush(p3, b), b.scale);
   const uint32_t top = (w + 0x01010101u) >> 7;     // bit 0 of each byte: that byte was 0x7f
-  return w & ~(top & 0x01010101u);
+  return w ^ (top & 0x01010101u);                  // 0x7f -> 0x7e, other bytes unchanged
 }
 
 // R1 E4M3 codes of four already scaled values of any sign (byte i = value i), on the

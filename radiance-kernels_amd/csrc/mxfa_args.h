@@ -13,6 +13,7 @@ struct FaArgs {
   float* o;
   float* part_o;      // decode: partial O  [B*Hq][nparts][D]
   float* part_ml;     // decode: partial (m, l) [B*Hq][nparts][2]
+  const uint8_t* kbf; // prefill: bf16 copy of K [B][Hkv][Sk][D] (mxfa_k_to_bf16)
   int B, Hq, Hkv, Sq, Sk;
   int Skc;            // keys allocated per (b, KV head) in k/ks/v/vs (>= Sk; base offsets use it)
   int q_pos0, window, causal, v_e3m2;

@@ -47,6 +47,12 @@ const char* const kKernelNames[] = {
     "mxfa_prefill_d128_softcap_r2", "mxfa_prefill_d256_softcap_r2", "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
     "mxfa_decode_d256_r2",     "mxfa_decode_d64_softcap_r2", "mxfa_decode_d128_softcap_r2",
     "mxfa_decode_d256_softcap_r2", "mxfa_gemm", "mxfa_gemm_ae3m2", "mxfa_gemm_be3m2", "mxfa_gemm_ae3m2_be3m2",
+    "mxfa_prefill_pipe_d64",   "mxfa_prefill_pipe_d128",  "mxfa_prefill_pipe_d64_softcap", "mxfa_prefill_pipe_d128_softcap",
+    "mxfa_prefill_pipe_d64_r2", "mxfa_prefill_pipe_d128_r2", "mxfa_prefill_pipe_d64_softcap_r2",
+    "mxfa_prefill_pipe_d128_softcap_r2",
+    "mxfa_k_to_bf16",          "mxfa_prefill3_d64",       "mxfa_prefill3_d128",   "mxfa_prefill3_d64_softcap",
+    "mxfa_prefill3_d128_softcap", "mxfa_prefill3_d64_r2", "mxfa_prefill3_d128_r2", "mxfa_prefill3_d64_softcap_r2",
+    "mxfa_prefill3_d128_softcap_r2",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -422,6 +428,39 @@ mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p
   return launch(dm, "mxfa_fill_normal_f32", grid, dim3(256), args, stream);
 }
 
+}  // extern "C"
+
+namespace {
+// Workgroup shape of the prefill kernels: hpw query heads (of one KV head) per workgroup,
+// 4 / hpw 32-query waves each.
+FaArgs prefill_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
+                    const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, dim3& grid) {
+  FaArgs a = make_args(p, q, q_sc, k, k_sc, v, v_sc, o);
+  a.hpw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
+  a.qpw = 32 * (4 / a.hpw);
+  a.n_qblk = (p->seq_q + a.qpw - 1) / a.qpw;
+  grid = dim3((unsigned)a.n_qblk, (unsigned)(p->batch * p->num_kv_heads * (a.group / a.hpw)));
+  return a;
+}
+
+// Shapes that the three-waves-per-SIMD kernel serves (with its bf16 K workspace).
+bool prefill3_shape(const mxfa_attn_params* p) { return p->head_dim <= 128 && p->v_fmt == MXFA_FMT_E4M3; }
+
+size_t prefill3_workspace(const mxfa_attn_params* p) {
+  return (size_t)p->batch * p->num_kv_heads * p->seq_k * p->head_dim * 2;
+}
+
+// MXFA_PREFILL=staged or =pipe selects that kernel for every call (both workspace-free);
+// the switch exists to compare the kernels, which give O within the oracle's tolerance.
+const char* prefill_override() {
+  const char* sel = getenv("MXFA_PREFILL");
+  if (sel && (std::strcmp(sel, "staged") == 0 || std::strcmp(sel, "pipe") == 0)) return sel;
+  return nullptr;
+}
+}  // namespace
+
+extern "C" {
+
 mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
                          const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* stream) {
   if (mxfa_status st = check_params(p, false)) return st;
@@ -429,13 +468,49 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
-  FaArgs a = make_args(p, q, q_sc, k, k_sc, v, v_sc, o);
-  a.hpw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
-  a.qpw = 32 * (4 / a.hpw);
-  a.n_qblk = (p->seq_q + a.qpw - 1) / a.qpw;
-  dim3 grid((unsigned)a.n_qblk, (unsigned)(p->batch * p->num_kv_heads * (a.group / a.hpw)));
+  dim3 grid;
+  FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, grid);
   void* args[] = {&a};
-  return launch(dm, kernel_name("prefill", p), grid, dim3(256), args, stream);
+  // D <= 128 with E4M3 V: the software-pipelined kernel (LDS-DMA staging, score MFMAs of
+  // the next block inside the softmax); D = 256 and E3M2 V: the staged kernel.
+  const char* sel = prefill_override();
+  const bool staged = (sel && std::strcmp(sel, "staged") == 0) || !prefill3_shape(p);
+  return launch(dm, kernel_name(staged ? "prefill" : "prefill_pipe", p), grid, dim3(256), args, stream);
+}
+
+mxfa_status mxfa_prefill_plan(const mxfa_attn_params* p, size_t* workspace_bytes) {
+  if (mxfa_status st = check_params(p, false)) return st;
+  if (!workspace_bytes) return fail(MXFA_ERR_INVALID_ARG, "workspace_bytes is NULL");
+  *workspace_bytes = prefill3_shape(p) ? prefill3_workspace(p) : 0;
+  return MXFA_OK;
+}
+
+mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
+                            const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (mxfa_status st = check_params(p, false)) return st;
+  if (!prefill3_shape(p) || prefill_override()) return mxfa_prefill(p, q, q_sc, k, k_sc, v, v_sc, o, stream);
+  const void* ptrs[] = {q, q_sc, k, k_sc, v, v_sc, o};
+  if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
+  const size_t need = prefill3_workspace(p);
+  if (!workspace || workspace_bytes < need)
+    return fail(MXFA_ERR_WORKSPACE, "prefill workspace needs " + std::to_string(need) + " bytes");
+  if (!aligned16(workspace)) return fail(MXFA_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
+  dim3 grid;
+  FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, grid);
+  a.kbf = static_cast<const uint8_t*>(workspace);
+  // bf16 K: one thread per 16 codes
+  int64_t rows = (int64_t)p->batch * p->num_kv_heads * p->seq_k;
+  int D = p->head_dim, Sk = p->seq_k, Skc = a.Skc;
+  uint8_t* kbf = static_cast<uint8_t*>(workspace);
+  void* cargs[] = {(void*)&k, (void*)&k_sc, &rows, &D, &Sk, &Skc, &kbf};
+  if (mxfa_status st =
+          launch(dm, "mxfa_k_to_bf16", dim3((unsigned)((rows * (D / 16) + 255) / 256)), dim3(256), cargs, stream))
+    return st;
+  void* args[] = {&a};
+  return launch(dm, kernel_name("prefill3", p), grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* n_parts, size_t* workspace_bytes) {

@@ -101,8 +101,8 @@ class GemmParams(ctypes.Structure):
                 ("a_fmt", ctypes.c_int32), ("b_fmt", ctypes.c_int32), ("c_fmt", ctypes.c_int32)]
 
 
-EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
-           "mxfa_decode_noalloc",
+EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_prefill_plan",
+           "mxfa_prefill_ws", "mxfa_decode_plan", "mxfa_decode", "mxfa_decode_noalloc",
            "mxfa_kv_append", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
            "mxfa_last_error", "mxfa_version", "mxfa_gemm")
 
@@ -122,6 +122,8 @@ def lib():
         L.mxfa_quantize_cols.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int, u8p, u8p, vp]
         L.mxfa_quantize_rows_r4.argtypes = [f32p, ctypes.c_int64, ctypes.c_int32, u8p, u8p, vp]
         L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
+        L.mxfa_prefill_plan.argtypes = [P(AttnParams), P(ctypes.c_size_t)]
+        L.mxfa_prefill_ws.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
         L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
         L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
         L.mxfa_decode_noalloc.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
@@ -134,7 +136,8 @@ def lib():
         L.mxfa_status_string.restype = ctypes.c_char_p
         L.mxfa_last_error.restype = ctypes.c_char_p
         L.mxfa_version.restype = ctypes.c_int32
-        for name in ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_decode_plan", "mxfa_decode",
+        for name in ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill",
+                     "mxfa_prefill_plan", "mxfa_prefill_ws", "mxfa_decode_plan", "mxfa_decode",
                      "mxfa_decode_noalloc", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_kv_append", "mxfa_gemm"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
@@ -245,15 +248,30 @@ def fill_normal(x, seed, outlier_p=0.0, outlier_mul=20.0, stream=None):
     return x
 
 
-def prefill(p, q, qs, k, ks, v, vs, out=None, stream=None):
-    """O [B, Hq, Sq, D] fp32 of MXFP8 attention (mxfa_prefill); operands in the C-ABI layouts
-    (k/v/k_sc/v_sc with p.kv_stride keys per (batch, KV head) when it is set)."""
+def prefill_plan(p):
+    """Workspace bytes of mxfa_prefill_ws for p (0: the shape runs the workspace-free kernel)."""
+    ws = ctypes.c_size_t(0)
+    _check(lib().mxfa_prefill_plan(ctypes.byref(p), ctypes.byref(ws)))
+    return ws.value
+
+
+def prefill(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):
+    """O [B, Hq, Sq, D] fp32 of MXFP8 attention; operands in the C-ABI layouts (k/v/k_sc/v_sc
+    with p.kv_stride keys per (batch, KV head) when it is set).  workspace: None allocates
+    prefill_plan(p) bytes and calls mxfa_prefill_ws; a uint8 CUDA tensor is passed to
+    mxfa_prefill_ws; False calls mxfa_prefill (no workspace)."""
     import torch
     if out is None:
         out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device=q.device)
     _check_attn_operands(p, q, qs, k, ks, v, vs, out)
-    _check(lib().mxfa_prefill(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out),
-                              _stream(stream)))
+    args = (ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), _ptr(out))
+    if workspace is False:
+        _check(lib().mxfa_prefill(*args, _stream(stream)))
+        return out
+    if workspace is None:
+        workspace = torch.empty(max(prefill_plan(p), 16), dtype=torch.uint8, device=q.device)
+    _need(workspace, torch.uint8, (workspace.numel(),), "workspace")
+    _check(lib().mxfa_prefill_ws(*args, _ptr(workspace), workspace.numel(), _stream(stream)))
     return out
 
 

@@ -32,13 +32,14 @@ def test_code_object_present_and_for_gfx950():
     assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     assert b"gfx950" in data
     for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows",
-              "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2", "mxfa_decode_scratch"):
+              "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2", "mxfa_decode_scratch", "mxfa_k_to_bf16",
+              "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill_pipe_d128"):
         assert k.encode() in data
 
 
 def test_version_and_status_strings():
     L = mxfa.lib()
-    assert L.mxfa_version() == 2
+    assert L.mxfa_version() == 3
     assert L.mxfa_status_string(0) == b"ok"
     assert L.mxfa_status_string(5) == b"workspace too small"
 
@@ -162,3 +163,25 @@ def test_decode_noalloc_rejects_before_touching_the_device():
     ok = mxfa.make_params(64, 32, 8, 1, 8192, 128, causal=True, q_pos0=8191)
     assert mxfa.decode_plan(ok)[1] <= mxfa.DECODE_SCRATCH_BYTES
     assert L.mxfa_decode_noalloc(ctypes.byref(ok), None, None, None, None, None, None, None, None) == 1
+
+
+def test_prefill_plan_and_workspace_checks():
+    """mxfa_prefill_plan: the bf16 K copy (B * Hkv * Sk * D * 2 bytes) for D <= 128 with E4M3 V,
+    0 for D = 256 or E3M2 V; mxfa_prefill_ws rejects a missing or short workspace with
+    MXFA_ERR_WORKSPACE before touching the device."""
+    L = mxfa.lib()
+    p = mxfa.make_params(2, 32, 8, 4096, 4096, 128, causal=True)
+    assert mxfa.prefill_plan(p) == 2 * 8 * 4096 * 128 * 2
+    assert mxfa.prefill_plan(mxfa.make_params(1, 4, 2, 64, 4096, 64, kv_stride=8192)) == 2 * 4096 * 64 * 2
+    assert mxfa.prefill_plan(mxfa.make_params(1, 16, 8, 128, 128, 256)) == 0
+    assert mxfa.prefill_plan(mxfa.make_params(1, 4, 2, 64, 64, 128, v_fmt=mxfa.FMT_E3M2)) == 0
+    assert L.mxfa_prefill_plan(ctypes.byref(p), None) == 1
+    assert L.mxfa_prefill_plan(ctypes.byref(mxfa.make_params(1, 3, 2, 32, 64, 64)), ctypes.byref(ctypes.c_size_t())) == 1
+    buf = (ctypes.c_uint8 * 64)()
+    ptr = ctypes.c_void_p(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16)
+    small = mxfa.make_params(1, 2, 2, 32, 64, 64)
+    need = mxfa.prefill_plan(small)
+    assert L.mxfa_prefill_ws(ctypes.byref(small), *([ptr] * 7), None, need, None) == 5
+    assert L.mxfa_prefill_ws(ctypes.byref(small), *([ptr] * 7), ptr, need - 1, None) == 5
+    assert b"workspace needs" in L.mxfa_last_error()
+    assert L.mxfa_prefill_ws(ctypes.byref(small), *([None] * 7), ptr, need, None) == 1

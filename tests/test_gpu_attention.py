@@ -30,7 +30,11 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
                          v_fmt=v_fmt, p_rule=p_rule)
     out = torch.full((B, Hq, Sq, D), float("nan"), dtype=torch.float32, device=DEV)
     mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
+    # the workspace-free kernel (mxfa_prefill) runs the same arithmetic in the same order
+    out_nw = torch.full_like(out, float("nan"))
+    mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out_nw, workspace=False)
     torch.cuda.synchronize()
+    assert torch.equal(out, out_nw), "mxfa_prefill_ws and mxfa_prefill differ"
     o = np_(out)
     assert np.all(np.isfinite(o)), "coverage: some O elements were not written"
     want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
