@@ -1085,17 +1085,54 @@ __device__ __forceinline__ void pipe_interleave() {
 
 // Softmax and P requant of one block's scores (in place: s holds the scores, masked and
 // capped): updates m and l, returns the PV operand codes and scales and the O correction.
-// max(a, b) as one v_max_f32 (fmaxf would first canonicalize operands the compiler cannot
-// prove canonical, such as cross-lane swap results; the scores are never signaling NaNs).
-__device__ __forceinline__ float vmax(float a, float b) {
+// max(a, b) without the canonicalizing maxes fmaxf adds on operands the compiler cannot prove
+// canonical (MFMA results, cross-lane swaps): IEEE maximum (v_maximum3_f32 on gfx950; a NaN
+// score, possible only from NaN operand codes, propagates instead of being dropped).
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// max of the 16 scores of one S^T tile held by a lane
+__device__ __forceinline__ float tile_max16(const v16f& x) {
+  float m = vmax(x[0], x[1]);
+#pragma unroll
+  for (int i = 2; i < 16; i++) m = vmax(m, x[i]);
+  return m;
+}
+
+// A wave-uniform value in a VGPR: VALU instructions whose operands are all VGPRs issue at
+// the full rate, one with a scalar operand at half of it.
+__device__ __forceinline__ float in_vgpr(float x) {
   float r;
-  __asm__("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  __asm__("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
   return r;
+}
+__device__ __forceinline__ uint32_t in_vgpr_u(uint32_t x) {
+  uint32_t r;
+  __asm__("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
+  return r;
+}
+
+// fp32 subnormal results flushed to zero (MODE.FP_DENORM single-precision bits = 0) for the
+// rest of the wave.  The pipelined prefill kernels rely on it for the R1 flush of P (below);
+// elsewhere it only turns results below 2^-126 into zeros.
+__device__ __forceinline__ void fp32_flush_denormals() {
+  __builtin_amdgcn_s_setreg((1 << 11) | (4 << 6) | 1, 0);   // hwreg(MODE, 4, 2)
 }
 
 __device__ __forceinline__ float pair_max_raw(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// R1 codes of four P values of a tile with scale code sc, given y = P * 2^(7 - sc) computed
+// with fp32 subnormals flushed (fp32_flush_denormals): the R1 flush bound of the tile,
+// F4M3 * 2^(sc - 127), is within two ulps below 2^(sc - 133), the bound that the flush to zero
+// applies (y < 2^-126), and no exponential lands in between: sc <= 119 (amax <= 1), so
+// P = exp2(x) with x within 2^-19 of an integer e <= -14 is 2^e itself or at least ~10 ulps
+// from it.  The kept values convert as y * 2^120 = P / 2^(sc - 127), the same codes.
+__device__ __forceinline__ uint32_t p_pack4_ftz(float y0, float y1, float y2, float y3, uint32_t ones) {
+  const uint32_t w = cvt_pack4_in_place(y0, y1, y2, y3, __uint_as_float(7u << 23));   // 2^-120
+  const uint32_t top = (w + ones) >> 7;               // bit 0 of each byte: that byte was 0x7f
+  return w ^ (top & ones);                            // 0x7f -> 0x7e, other bytes unchanged
 }
 
 template <bool SOFTCAP, int PR>
@@ -1104,12 +1141,7 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
   constexpr int NT = BN / 32;
   float bmax[NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) {
-    float mx = fmaxf(s[t][0], s[t][1]);
-#pragma unroll
-    for (int i = 2; i < 16; i++) mx = fmaxf(mx, s[t][i]);
-    bmax[t] = pair_max_raw(mx);
-  }
+  for (int t = 0; t < NT; t++) bmax[t] = pair_max_raw(tile_max16(s[t]));
   float rmax = bmax[0];
 #pragma unroll
   for (int t = 1; t < NT; t++) rmax = vmax(rmax, bmax[t]);
@@ -1118,7 +1150,7 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
   corr = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mu) * c);
   m = m_new;
   const float mcn = -(mu * c);
-  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float part[4];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const float amax = __builtin_amdgcn_exp2f((bmax[t] - mu) * c);
@@ -1144,13 +1176,15 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
     } else {
 #pragma unroll
       for (int i = 0; i < 16; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], c, mcn));
-      const PTileBounds bnd = p_tile_bounds(sc);
+      const float f = __uint_as_float((134u - sc) << 23);     // 2^(7 - sc)
+      const uint32_t ones = in_vgpr_u(0x01010101u);
 #pragma unroll
-      for (int g = 0; g < 4; g++) w[g] = p_pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], bnd);
+      for (int g = 0; g < 4; g++)
+        w[g] = p_pack4_ftz(p[4 * g] * f, p[4 * g + 1] * f, p[4 * g + 2] * f, p[4 * g + 3] * f, ones);
     }
     // row-sum terms in four independent chains (no 32-deep add dependency)
 #pragma unroll
-    for (int i = 0; i < 16; i++) part[i & 3] += p[i];
+    for (int i = 0; i < 16; i++) part[i & 3] = (t == 0 && i < 4) ? p[i] : part[i & 3] + p[i];
 #pragma unroll
     for (int g = 0; g < 4; g++) pb[4 * (t & 1) + g] = (int)w[g];
   }
@@ -1222,6 +1256,7 @@ __device__ __forceinline__ void pipe_pv(v16f (&o)[D / 32], const PvRegs<D>& pr, 
 template <int D, bool SOFTCAP, int PR>
 __device__ void prefill_pipe_impl(const FaArgs& a) {
   using L = PipeLds<D>;
+  fp32_flush_denormals();   // pipe_softmax's R1 flush
   __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sKb1[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sK8[3][L::K8 + L::SCB];   // K8(j) in sK8[j % 3]
@@ -1269,7 +1304,7 @@ __device__ void prefill_pipe_impl(const FaArgs& a) {
 
   const KvRsrc rs = kv_rsrc<D>(a.k + (int64_t)bk * a.Skc * D, a.ks + (int64_t)bk * a.Skc * (D / 32),
                                a.v + (int64_t)bk * a.Skc * D, a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk);
-  const float c = SOFTCAP ? 1.0f : a.c_log2;
+  const float c = SOFTCAP ? 1.0f : in_vgpr(a.c_log2);
 
   v16f o[D / 32];
 #pragma unroll
@@ -1441,9 +1476,10 @@ struct P3Lane {
 };
 
 template <int D> __device__ __forceinline__ P3Lane p3_lane(int wave, int lane) {
-  constexpr int VRPI = 1024 / D;
-  const int row = wave * VRPI + lane / (D / 16), pos = lane % (D / 16);
-  return {(lane % 16) * (2 * D) + (lane / 16) * 16, (lane / (D / 16)) * D + ((pos ^ vsw<D>(row)) << 4)};
+  constexpr unsigned VRPI = 1024 / D, CPR = D / 16;
+  const unsigned ln = (unsigned)lane;
+  const unsigned row = (unsigned)wave * VRPI + ln / CPR, pos = ln % CPR;
+  return {(int)((ln % 16) * (2 * D) + (ln & 48u)), (int)((ln / CPR) * D + ((pos ^ (unsigned)vsw<D>((int)row)) << 4))};
 }
 
 // The DMA instructions of one key block (bf16 K into kb, V codes and scales into v): each
@@ -1494,6 +1530,7 @@ __device__ __forceinline__ int fresh_lane() {
 template <int D, bool SOFTCAP, int PR>
 __device__ void prefill3_impl(const FaArgs& a) {
   using L = P3Lds<D>;
+  fp32_flush_denormals();   // pipe_softmax's R1 flush
   __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sKb1[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sV0[L::V + L::SCB];
@@ -1536,7 +1573,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
 
   const KvRsrc rs = kv_rsrc<D>(a.k, a.ks, a.v + (int64_t)bk * a.Skc * D, a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk);
   const __amdgpu_buffer_rsrc_t rkb = buf_rsrc(a.kbf, (int64_t)bk * a.Sk * (2 * D), (int64_t)a.Sk * (2 * D));
-  const float c = SOFTCAP ? 1.0f : a.c_log2;
+  const float c = SOFTCAP ? 1.0f : in_vgpr(a.c_log2);
 
   v16f o[D / 32];
 #pragma unroll
