@@ -1182,7 +1182,8 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
       for (int g = 0; g < 4; g++)
         w[g] = p_pack4_ftz(p[4 * g] * f, p[4 * g + 1] * f, p[4 * g + 2] * f, p[4 * g + 3] * f, ones);
     }
-    // row-sum terms in four independent chains (no 32-deep add dependency)
+    // row-sum terms (every P, including those R1 flushes from the codes) in four
+    // independent chains (no 32-deep add dependency)
 #pragma unroll
     for (int i = 0; i < 16; i++) part[i & 3] = (t == 0 && i < 4) ? p[i] : part[i & 3] + p[i];
 #pragma unroll
@@ -1472,37 +1473,48 @@ template <int D> struct P3Lds {
 // depends on key bits that the wave index and the lane fix -- instructions of one wave are
 // 4 x 1024 / D rows apart, a multiple of 16).
 struct P3Lane {
-  int k, v;
+  int k, v, s;
 };
 
 template <int D> __device__ __forceinline__ P3Lane p3_lane(int wave, int lane) {
   constexpr unsigned VRPI = 1024 / D, CPR = D / 16;
   const unsigned ln = (unsigned)lane;
   const unsigned row = (unsigned)wave * VRPI + ln / CPR, pos = ln % CPR;
-  return {(int)((ln % 16) * (2 * D) + (ln & 48u)), (int)((ln / CPR) * D + ((pos ^ (unsigned)vsw<D>((int)row)) << 4))};
+  return {(int)((ln % 16) * (2 * D) + (ln & 48u)), (int)((ln / CPR) * D + ((pos ^ (unsigned)vsw<D>((int)row)) << 4)),
+          (int)(ln * 4)};
 }
 
+// Sources of the prefill3 DMA for one (b, KV head): bf16 K rows (2D bytes), V codes, V scales.
+struct P3Src {
+  const uint8_t *kbf, *v, *vs;
+  int Sk;
+};
+
 // The DMA instructions of one key block (bf16 K into kb, V codes and scales into v): each
-// wave issues instructions wave, wave + 4, ... of each tile, wave 3 the V scales.  The
-// instruction's part of each offset is wave-uniform (one VALU add per instruction).  Key
-// rows >= Sk read 0 (buffer resources bounded at Sk).
+// wave issues instructions wave, wave + 4, ... of each tile, wave 3 the V scales.  Each
+// instruction's buffer resource starts at its wave-uniform source offset and ends at key Sk
+// (built by scalar instructions; keys >= Sk read 0), so the vector offset is the lane part alone.
 template <int D>
-__device__ __forceinline__ void p3_dma(const __amdgpu_buffer_rsrc_t& rkb, const KvRsrc& rs, uint8_t* kb, uint8_t* v,
-                                       int key0, int wave, int lane, const P3Lane& pl) {
+__device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v, int key0, int wave, const P3Lane& pl) {
   using L = P3Lds<D>;
   constexpr int VRPI = 1024 / D;
   constexpr int IPG = 2 * D / 64;                  // K DMA instructions per 16-row group (4 chunks each)
 #pragma unroll
   for (int m = 0; m < L::KDMA / NWAVE; m++) {
     const int i = wave + NWAVE * m;
-    dma_lds<16>(rkb, kb + i * 1024, pl.k + ((key0 + (i / IPG) * 16) * (2 * D) + (i % IPG) * 64));
+    const int off = (key0 + (i / IPG) * 16) * (2 * D) + (i % IPG) * 64;
+    dma_lds<16>(buf_rsrc(src.kbf, off, (int64_t)src.Sk * (2 * D) - off), kb + i * 1024, pl.k);
   }
 #pragma unroll
   for (int m = 0; m < L::VDMA / NWAVE; m++) {
     const int i = wave + NWAVE * m;
-    dma_lds<16>(rs.v, v + i * 1024, pl.v + (key0 + i * VRPI) * D);
+    const int off = (key0 + i * VRPI) * D;
+    dma_lds<16>(buf_rsrc(src.v, off, (int64_t)src.Sk * D - off), v + i * 1024, pl.v);
   }
-  if (wave == 3) dma_lds<4>(rs.vs, v + L::V, (key0 / 32) * D + lane * 4);
+  if (wave == 3) {
+    const int off = (key0 / 32) * D;
+    dma_lds<4>(buf_rsrc(src.vs, off, (int64_t)(src.Sk / 32) * D - off), v + L::V, pl.s);
+  }
 }
 
 template <int D>
@@ -1571,8 +1583,9 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const int wq_lo = a.q_pos0 + qw0, wq_hi = a.q_pos0 + min(qw0 + 31, a.Sq - 1);
   const bool wave_live = qw0 < a.Sq;
 
-  const KvRsrc rs = kv_rsrc<D>(a.k, a.ks, a.v + (int64_t)bk * a.Skc * D, a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk);
-  const __amdgpu_buffer_rsrc_t rkb = buf_rsrc(a.kbf, (int64_t)bk * a.Sk * (2 * D), (int64_t)a.Sk * (2 * D));
+  const P3Src src = {a.kbf + (int64_t)bk * a.Sk * (2 * D), a.v + (int64_t)bk * a.Skc * D,
+                     a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk};
+  const P3Lane pl = p3_lane<D>(wave, lane);
   const float c = SOFTCAP ? 1.0f : in_vgpr(a.c_log2);
 
   v16f o[D / 32];
@@ -1587,7 +1600,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
         (qw0 + 31 >= a.Sq) || !wave_live);
   };
 
-  if (j0 < j1) p3_dma<D>(rkb, rs, sKb0, sV0, j0 * BN, wave, lane, p3_lane<D>(wave, lane));
+  if (j0 < j1) p3_dma<D>(src, sKb0, sV0, j0 * BN, wave, pl);
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
   __syncthreads();
 
@@ -1597,11 +1610,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
     uint8_t* kb_dma = ST ? sKb0 : sKb1;
     uint8_t* v_cur = ST ? sV1 : sV0;
     uint8_t* v_dma = ST ? sV0 : sV1;
-    // lane-derived addresses are recomputed per use (fresh_lane) rather than held
-    if (j + 1 < j1) {
-      const int ln = fresh_lane();
-      p3_dma<D>(rkb, rs, kb_dma, v_dma, (j + 1) * BN, wave, ln, p3_lane<D>(wave, ln));
-    }
+    if (j + 1 < j1) p3_dma<D>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
     v16f sc[BN / 32];
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
     pipe_scores<SOFTCAP>(sc, a);
