@@ -972,14 +972,15 @@ __device__ __forceinline__ lds_void* lds_addr(const void* p) {
   return (lds_void*)(uint32_t)(uintptr_t)p;
 }
 
+// soff: a wave-uniform byte offset added to the source address (not to the LDS address)
 template <int SIZE>
-__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds_base, int voff) {
+__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds_base, int voff, int soff = 0) {
   if constexpr (SIZE == 16)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 16, voff, soff, 0, 0);
   else if constexpr (SIZE == 4)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 4, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 4, voff, soff, 0, 0);
   else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 2, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 2, voff, soff, 0, 0);
 }
 
 // The DMA instructions of one key block: fp8 K (do_k) into k8, V (do_v) into v; each wave
@@ -1468,20 +1469,27 @@ template <int D> struct P3Lds {
   static constexpr int SCB = 256;                 // V scales slot
 };
 
-// Per-lane parts of the DMA source offsets (the same for every instruction of a wave: a K
-// instruction covers 16 rows x 4 chunks, a V instruction 1024 / D whole rows, whose swizzle
-// depends on key bits that the wave index and the lane fix -- instructions of one wave are
-// 4 x 1024 / D rows apart, a multiple of 16).
+// DMA of one key block into the prefill3 tiles.  Wave w brings K rows 16w .. 16w + 15 (one
+// 16-row group of the chunk-major tile, 2D / 64 instructions of four 16-byte chunks per row)
+// and V instructions i0(w), i0(w) + 2 (D = 128; 8 rows each; i0 = 4(w / 2) + w % 2, so both
+// share the swizzle bits of their rows) or i0 = w (D = 64; 16 rows), wave 3 the V scales.
+// Per block the three buffer resources start at the block and end at key Sk (keys >= Sk
+// read 0); the vector offsets are loop-invariant lane parts, the K instructions' column
+// offset a scalar offset (within a row, so the range check sees the row either way).
 struct P3Lane {
   int k, v, s;
 };
 
+template <int D> __device__ __forceinline__ int p3_v_i0(int wave) {
+  return D == 128 ? 4 * (wave >> 1) + (wave & 1) : wave;
+}
+
 template <int D> __device__ __forceinline__ P3Lane p3_lane(int wave, int lane) {
   constexpr unsigned VRPI = 1024 / D, CPR = D / 16;
-  const unsigned ln = (unsigned)lane;
-  const unsigned row = (unsigned)wave * VRPI + ln / CPR, pos = ln % CPR;
-  return {(int)((ln % 16) * (2 * D) + (ln & 48u)), (int)((ln / CPR) * D + ((pos ^ (unsigned)vsw<D>((int)row)) << 4)),
-          (int)(ln * 4)};
+  const unsigned ln = (unsigned)lane, w = (unsigned)wave;
+  const unsigned vrow = (unsigned)p3_v_i0<D>(wave) * VRPI + ln / CPR, pos = ln % CPR;
+  return {(int)((16 * w + ln % 16) * (2 * D) + (ln / 16) * 16),
+          (int)(vrow * D + ((pos ^ (unsigned)vsw<D>((int)vrow)) << 4)), (int)(ln * 4)};
 }
 
 // Sources of the prefill3 DMA for one (b, KV head): bf16 K rows (2D bytes), V codes, V scales.
@@ -1490,30 +1498,39 @@ struct P3Src {
   int Sk;
 };
 
-// The DMA instructions of one key block (bf16 K into kb, V codes and scales into v): each
-// wave issues instructions wave, wave + 4, ... of each tile, wave 3 the V scales.  Each
-// instruction's buffer resource starts at its wave-uniform source offset and ends at key Sk
-// (built by scalar instructions; keys >= Sk read 0), so the vector offset is the lane part alone.
-template <int D>
+template <int D, bool DO_K = true, bool DO_V = true>
 __device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v, int key0, int wave, const P3Lane& pl) {
   using L = P3Lds<D>;
-  constexpr int VRPI = 1024 / D;
-  constexpr int IPG = 2 * D / 64;                  // K DMA instructions per 16-row group (4 chunks each)
+  constexpr int IPG = 2 * D / 64;                  // K instructions per 16-row group
+  if constexpr (DO_K) {
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(src.kbf, (int64_t)key0 * (2 * D), (int64_t)(src.Sk - key0) * (2 * D));
 #pragma unroll
-  for (int m = 0; m < L::KDMA / NWAVE; m++) {
-    const int i = wave + NWAVE * m;
-    const int off = (key0 + (i / IPG) * 16) * (2 * D) + (i % IPG) * 64;
-    dma_lds<16>(buf_rsrc(src.kbf, off, (int64_t)src.Sk * (2 * D) - off), kb + i * 1024, pl.k);
+    for (int m = 0; m < IPG; m++) dma_lds<16>(rk, kb + wave * (32 * D) + m * 1024, pl.k, 64 * m);
   }
-#pragma unroll
-  for (int m = 0; m < L::VDMA / NWAVE; m++) {
-    const int i = wave + NWAVE * m;
-    const int off = (key0 + i * VRPI) * D;
-    dma_lds<16>(buf_rsrc(src.v, off, (int64_t)src.Sk * D - off), v + i * 1024, pl.v);
-  }
-  if (wave == 3) {
+  if constexpr (DO_V) {
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(src.v, (int64_t)key0 * D, (int64_t)(src.Sk - key0) * D);
+    const int i0 = p3_v_i0<D>(wave);
+    dma_lds<16>(rv, v + i0 * 1024, pl.v);
+    if constexpr (D == 128) dma_lds<16>(rv, v + (i0 + 2) * 1024, pl.v + 2048);
+    // the V scales (one dword instruction): every wave issues it, writing the same bytes, so
+    // the sequence has no branch
     const int off = (key0 / 32) * D;
     dma_lds<4>(buf_rsrc(src.vs, off, (int64_t)(src.Sk / 32) * D - off), v + L::V, pl.s);
+  }
+}
+
+// Schedule of the score MFMAs with the next block's DMA: after the first two K operand
+// reads, per MFMA one more read, two scalar instructions and a DMA instruction, so the wave
+// issues the DMA while the matrix pipe works instead of before it.
+template <int D>
+__device__ __forceinline__ void p3_dma_interleave() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);      // DS reads
+#pragma unroll
+  for (int k = 0; k < D / 16 * (BN / 32); k++) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x004, 2, 0);    // SALU
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read (LDS DMA)
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read
   }
 }
 
@@ -1610,9 +1627,12 @@ __device__ void prefill3_impl(const FaArgs& a) {
     uint8_t* kb_dma = ST ? sKb0 : sKb1;
     uint8_t* v_cur = ST ? sV1 : sV0;
     uint8_t* v_dma = ST ? sV0 : sV1;
-    if (j + 1 < j1) p3_dma<D>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+    // the DMA instructions of block j+1 are issued between the score MFMAs of block j (also
+    // past the last block: keys >= Sk read 0, and nothing reads that stage)
     v16f sc[BN / 32];
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
+    p3_dma<D>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+    p3_dma_interleave<D>();
     pipe_scores<SOFTCAP>(sc, a);
     if (need_mask(j)) {
       const int ln = fresh_lane();
@@ -1666,6 +1686,7 @@ MXFA_PREFILL3(64, false, P_R2, mxfa_prefill3_d64_r2)
 MXFA_PREFILL3(128, false, P_R2, mxfa_prefill3_d128_r2)
 MXFA_PREFILL3(64, true, P_R2, mxfa_prefill3_d64_softcap_r2)
 MXFA_PREFILL3(128, true, P_R2, mxfa_prefill3_d128_softcap_r2)
+
 
 // ---------------------------------------------------------------------------
 // Decode (q_len = 1, split-KV).  The 64-key blocks of each (b, KV head) are dealt to
