@@ -118,14 +118,15 @@ mxfa_status mxfa_prefill(const mxfa_attn_params *p,
                          const uint8_t *v, const uint8_t *v_sc,
                          float *o, void *stream);
 
-/* Prefill with a caller workspace: the faster path for head_dim <= 128 with E4M3 V.  A first
- * launch writes the bf16 value of every K element (E4M3 code x 2^(scale - 127), exact in bf16)
- * into the workspace; the attention kernel then streams that copy and V into LDS by DMA and
- * runs three waves per SIMD.  Same inputs, outputs and O as mxfa_prefill (within the same
- * tolerance of the reference's algorithm; the two kernels order no sum differently, but the
- * bf16 K operand is exact in both).  *workspace_bytes = batch * num_kv_heads * seq_k *
- * head_dim * 2 for those shapes, 0 for the others (then mxfa_prefill_ws runs mxfa_prefill and
- * ignores the workspace).  A workspace smaller than the plan is MXFA_ERR_WORKSPACE.
+/* Prefill with a caller workspace, the faster path for every shape.  First launches write the
+ * bf16 value of every K element (E4M3 code x 2^(scale - 127), exact in bf16) and, for E3M2 V,
+ * the E4M3 code of every V element (the same value) into the workspace; the attention kernel
+ * then streams those copies into LDS by DMA: three 4-wave workgroups per CU for head_dim <= 128,
+ * one 8-wave workgroup (two waves per SIMD) for head_dim 256.  Same inputs, outputs and O as
+ * mxfa_prefill within the tolerance of the reference's algorithm (bit-identical to it for
+ * head_dim <= 128 with E4M3 V, where both run the same arithmetic in the same order).
+ * *workspace_bytes = batch * num_kv_heads * seq_k * head_dim * (2, or 3 with E3M2 V).  A
+ * workspace smaller than the plan is MXFA_ERR_WORKSPACE.
  * Replaces the same reference entry point as mxfa_prefill (kernels/flash_attention_mx_gqa/
  * kernel.cpp:91-191); the reference's matrix unit takes K's codes and scales as they are, so
  * it has no such copy: the workspace is this library's operand layout for the bf16 score MFMA. */

@@ -53,6 +53,8 @@ const char* const kKernelNames[] = {
     "mxfa_k_to_bf16",          "mxfa_prefill3_d64",       "mxfa_prefill3_d128",   "mxfa_prefill3_d64_softcap",
     "mxfa_prefill3_d128_softcap", "mxfa_prefill3_d64_r2", "mxfa_prefill3_d128_r2", "mxfa_prefill3_d64_softcap_r2",
     "mxfa_prefill3_d128_softcap_r2",
+    "mxfa_prefill3_d256",      "mxfa_prefill3_d256_softcap", "mxfa_prefill3_d256_r2", "mxfa_prefill3_d256_softcap_r2",
+    "mxfa_v_to_e4m3",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -431,23 +433,33 @@ mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p
 }  // extern "C"
 
 namespace {
-// Workgroup shape of the prefill kernels: hpw query heads (of one KV head) per workgroup,
-// 4 / hpw 32-query waves each.
+// Workgroup shape of the prefill kernels: nw waves (4, or 8 for the D = 256 workspace
+// kernel), hpw query heads (of one KV head) per workgroup, nw / hpw 32-query waves each.
 FaArgs prefill_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
-                    const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, dim3& grid) {
+                    const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, int nw, dim3& grid) {
   FaArgs a = make_args(p, q, q_sc, k, k_sc, v, v_sc, o);
-  a.hpw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
-  a.qpw = 32 * (4 / a.hpw);
+  a.hpw = 1;
+  for (int h = nw; h > 1; h /= 2)
+    if (a.group % h == 0) {
+      a.hpw = h;
+      break;
+    }
+  a.qpw = 32 * (nw / a.hpw);
   a.n_qblk = (p->seq_q + a.qpw - 1) / a.qpw;
   grid = dim3((unsigned)a.n_qblk, (unsigned)(p->batch * p->num_kv_heads * (a.group / a.hpw)));
   return a;
 }
 
-// Shapes that the three-waves-per-SIMD kernel serves (with its bf16 K workspace).
-bool prefill3_shape(const mxfa_attn_params* p) { return p->head_dim <= 128 && p->v_fmt == MXFA_FMT_E4M3; }
+// Waves per workgroup of the workspace kernel (mxfa_prefill3_*).
+int prefill3_waves(const mxfa_attn_params* p) { return p->head_dim == 256 ? 8 : 4; }
 
-size_t prefill3_workspace(const mxfa_attn_params* p) {
+// Workspace of mxfa_prefill_ws: the bf16 copy of K, then (E3M2 V) the E4M3 copy of V.
+size_t prefill3_kbf_bytes(const mxfa_attn_params* p) {
   return (size_t)p->batch * p->num_kv_heads * p->seq_k * p->head_dim * 2;
+}
+size_t prefill3_workspace(const mxfa_attn_params* p) {
+  const size_t v = p->v_fmt == MXFA_FMT_E3M2 ? (size_t)p->batch * p->num_kv_heads * p->seq_k * p->head_dim : 0;
+  return prefill3_kbf_bytes(p) + v;
 }
 
 // MXFA_PREFILL=staged or =pipe selects that kernel for every call (both workspace-free);
@@ -469,19 +481,19 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
   dim3 grid;
-  FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, grid);
+  FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, 4, grid);
   void* args[] = {&a};
   // D <= 128 with E4M3 V: the software-pipelined kernel (LDS-DMA staging, score MFMAs of
   // the next block inside the softmax); D = 256 and E3M2 V: the staged kernel.
   const char* sel = prefill_override();
-  const bool staged = (sel && std::strcmp(sel, "staged") == 0) || !prefill3_shape(p);
+  const bool staged = (sel && std::strcmp(sel, "staged") == 0) || p->head_dim > 128 || p->v_fmt != MXFA_FMT_E4M3;
   return launch(dm, kernel_name(staged ? "prefill" : "prefill_pipe", p), grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_prefill_plan(const mxfa_attn_params* p, size_t* workspace_bytes) {
   if (mxfa_status st = check_params(p, false)) return st;
   if (!workspace_bytes) return fail(MXFA_ERR_INVALID_ARG, "workspace_bytes is NULL");
-  *workspace_bytes = prefill3_shape(p) ? prefill3_workspace(p) : 0;
+  *workspace_bytes = prefill3_workspace(p);
   return MXFA_OK;
 }
 
@@ -489,7 +501,7 @@ mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const u
                             const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* workspace,
                             size_t workspace_bytes, void* stream) {
   if (mxfa_status st = check_params(p, false)) return st;
-  if (!prefill3_shape(p) || prefill_override()) return mxfa_prefill(p, q, q_sc, k, k_sc, v, v_sc, o, stream);
+  if (prefill_override()) return mxfa_prefill(p, q, q_sc, k, k_sc, v, v_sc, o, stream);
   const void* ptrs[] = {q, q_sc, k, k_sc, v, v_sc, o};
   if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
   const size_t need = prefill3_workspace(p);
@@ -498,19 +510,25 @@ mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const u
   if (!aligned16(workspace)) return fail(MXFA_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
+  const int nw = prefill3_waves(p);
   dim3 grid;
-  FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, grid);
-  a.kbf = static_cast<const uint8_t*>(workspace);
-  // bf16 K: one thread per 16 codes
+  FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, nw, grid);
+  uint8_t* kbf = static_cast<uint8_t*>(workspace);
+  uint8_t* vws = p->v_fmt == MXFA_FMT_E3M2 ? kbf + prefill3_kbf_bytes(p) : nullptr;
+  a.kbf = kbf;
+  a.vws = vws;
+  // bf16 K (and E4M3 V): one thread per 16 codes
   int64_t rows = (int64_t)p->batch * p->num_kv_heads * p->seq_k;
   int D = p->head_dim, Sk = p->seq_k, Skc = a.Skc;
-  uint8_t* kbf = static_cast<uint8_t*>(workspace);
+  const dim3 cgrid((unsigned)((rows * (D / 16) + 255) / 256));
   void* cargs[] = {(void*)&k, (void*)&k_sc, &rows, &D, &Sk, &Skc, &kbf};
-  if (mxfa_status st =
-          launch(dm, "mxfa_k_to_bf16", dim3((unsigned)((rows * (D / 16) + 255) / 256)), dim3(256), cargs, stream))
-    return st;
+  if (mxfa_status st = launch(dm, "mxfa_k_to_bf16", cgrid, dim3(256), cargs, stream)) return st;
+  if (vws) {
+    void* vargs[] = {(void*)&v, &rows, &D, &Sk, &Skc, &vws};
+    if (mxfa_status st = launch(dm, "mxfa_v_to_e4m3", cgrid, dim3(256), vargs, stream)) return st;
+  }
   void* args[] = {&a};
-  return launch(dm, kernel_name("prefill3", p), grid, dim3(256), args, stream);
+  return launch(dm, kernel_name("prefill3", p), grid, dim3((unsigned)(64 * nw)), args, stream);
 }
 
 mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* n_parts, size_t* workspace_bytes) {

@@ -963,6 +963,7 @@ template <int D> struct PipeLds {
 // ds_read_b64_tr_b8 reads of the PV operand (16 keys x 32 bytes per instruction) then hit
 // distinct banks, with no row padding (so a 1 KB DMA instruction fills whole rows).
 template <int D> __device__ __forceinline__ int vsw(int key) {
+  if constexpr (D == 256) return 2 * ((key & 3) | (((key >> 3) & 1) << 2));   // rows alias all 64 banks
   return D == 128 ? 2 * (((key >> 1) & 1) | ((key >> 2) & 2)) : ((key & 1) | (((key >> 3) & 1) << 1));
 }
 
@@ -1466,56 +1467,67 @@ template <int D> struct P3Lds {
   static constexpr int KDMA = KB / 1024;          // DMA instructions per K tile
   static constexpr int V = BN * D;                // V tile (swizzled as PipeLds)
   static constexpr int VDMA = V / 1024;
-  static constexpr int SCB = 256;                 // V scales slot
+  static constexpr int SCB = 2 * D > 256 ? 2 * D : 256;   // V scales [BN / 32][D], dword DMA
 };
 
-// DMA of one key block into the prefill3 tiles.  Wave w brings K rows 16w .. 16w + 15 (one
-// 16-row group of the chunk-major tile, 2D / 64 instructions of four 16-byte chunks per row)
-// and V instructions i0(w), i0(w) + 2 (D = 128; 8 rows each; i0 = 4(w / 2) + w % 2, so both
-// share the swizzle bits of their rows) or i0 = w (D = 64; 16 rows), wave 3 the V scales.
-// Per block the three buffer resources start at the block and end at key Sk (keys >= Sk
-// read 0); the vector offsets are loop-invariant lane parts, the K instructions' column
-// offset a scalar offset (within a row, so the range check sees the row either way).
+// Waves per prefill3 workgroup: 4 (three workgroups per CU) for D <= 128; 8 for D = 256,
+// whose double-buffered tiles (97 KB) allow one workgroup per CU -- two waves per SIMD.
+template <int D> struct P3Waves { static constexpr int N = D == 256 ? 8 : 4; };
+
+// DMA of one key block into the prefill3 tiles by NW waves.  K: the four 16-row groups of the
+// chunk-major tile, NW / 4 waves per group, each issuing 2D / 64 / (NW / 4) instructions of
+// four 16-byte chunks per row (wave-uniform column offset as the scalar offset, within a
+// row, so the range check sees the row either way).  V: VDMA / NW instructions per wave
+// whose rows share the swizzle bits (D = 128: i0 = 4(w / 2) + w % 2 and i0 + 2; D = 256:
+// 2w and 2w + 1; D = 64: w).  V scales: every wave issues the same dword instructions (same
+// bytes), so the sequence has no branch.  Per block the buffer resources start at the
+// block and end at key Sk (keys >= Sk read 0); the vector offsets are loop-invariant.
 struct P3Lane {
   int k, v, s;
 };
 
 template <int D> __device__ __forceinline__ int p3_v_i0(int wave) {
+  if constexpr (D == 256) return 2 * wave;
   return D == 128 ? 4 * (wave >> 1) + (wave & 1) : wave;
 }
+template <int D> constexpr int p3_v_step() { return D == 128 ? 2 : 1; }   // between a wave's V instructions
 
-template <int D> __device__ __forceinline__ P3Lane p3_lane(int wave, int lane) {
-  constexpr unsigned VRPI = 1024 / D, CPR = D / 16;
+template <int D, int NW> __device__ __forceinline__ P3Lane p3_lane(int wave, int lane) {
+  constexpr unsigned VRPI = 1024 / D, CPR = D / 16, WPG = NW / 4, IPW = 2 * D / 64 / WPG;
   const unsigned ln = (unsigned)lane, w = (unsigned)wave;
   const unsigned vrow = (unsigned)p3_v_i0<D>(wave) * VRPI + ln / CPR, pos = ln % CPR;
-  return {(int)((16 * w + ln % 16) * (2 * D) + (ln / 16) * 16),
+  return {(int)((16 * (w / WPG) + ln % 16) * (2 * D) + (w % WPG) * IPW * 64 + (ln / 16) * 16),
           (int)(vrow * D + ((pos ^ (unsigned)vsw<D>((int)vrow)) << 4)), (int)(ln * 4)};
 }
 
-// Sources of the prefill3 DMA for one (b, KV head): bf16 K rows (2D bytes), V codes, V scales.
+// Sources of the prefill3 DMA for one (b, KV head): bf16 K rows (2D bytes), V codes
+// (E4M3), V scales.
 struct P3Src {
   const uint8_t *kbf, *v, *vs;
   int Sk;
 };
 
-template <int D, bool DO_K = true, bool DO_V = true>
+template <int D, int NW, bool DO_K = true, bool DO_V = true>
 __device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v, int key0, int wave, const P3Lane& pl) {
   using L = P3Lds<D>;
-  constexpr int IPG = 2 * D / 64;                  // K instructions per 16-row group
+  constexpr int WPG = NW / 4, IPW = 2 * D / 64 / WPG;   // waves per 16-row group, K instructions per wave
+  constexpr int VPW = L::VDMA / NW;                     // V instructions per wave
   if constexpr (DO_K) {
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(src.kbf, (int64_t)key0 * (2 * D), (int64_t)(src.Sk - key0) * (2 * D));
+    uint8_t* kdst = kb + (wave / WPG) * (32 * D) + (wave % WPG) * IPW * 1024;
 #pragma unroll
-    for (int m = 0; m < IPG; m++) dma_lds<16>(rk, kb + wave * (32 * D) + m * 1024, pl.k, 64 * m);
+    for (int m = 0; m < IPW; m++) dma_lds<16>(rk, kdst + m * 1024, pl.k, 64 * m);
   }
   if constexpr (DO_V) {
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(src.v, (int64_t)key0 * D, (int64_t)(src.Sk - key0) * D);
     const int i0 = p3_v_i0<D>(wave);
-    dma_lds<16>(rv, v + i0 * 1024, pl.v);
-    if constexpr (D == 128) dma_lds<16>(rv, v + (i0 + 2) * 1024, pl.v + 2048);
-    // the V scales (one dword instruction): every wave issues it, writing the same bytes, so
-    // the sequence has no branch
+#pragma unroll
+    for (int m = 0; m < VPW; m++)
+      dma_lds<16>(rv, v + (i0 + m * p3_v_step<D>()) * 1024, pl.v + m * p3_v_step<D>() * 1024);
     const int off = (key0 / 32) * D;
-    dma_lds<4>(buf_rsrc(src.vs, off, (int64_t)(src.Sk / 32) * D - off), v + L::V, pl.s);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src.vs, off, (int64_t)(src.Sk / 32) * D - off);
+#pragma unroll
+    for (int m = 0; m < (2 * D + 255) / 256; m++) dma_lds<4>(rs, v + L::V + m * 256, pl.s + m * 256);
   }
 }
 
@@ -1559,6 +1571,7 @@ __device__ __forceinline__ int fresh_lane() {
 template <int D, bool SOFTCAP, int PR>
 __device__ void prefill3_impl(const FaArgs& a) {
   using L = P3Lds<D>;
+  constexpr int NW = P3Waves<D>::N;
   fp32_flush_denormals();   // pipe_softmax's R1 flush
   __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sKb1[L::KB];
@@ -1600,9 +1613,11 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const int wq_lo = a.q_pos0 + qw0, wq_hi = a.q_pos0 + min(qw0 + 31, a.Sq - 1);
   const bool wave_live = qw0 < a.Sq;
 
-  const P3Src src = {a.kbf + (int64_t)bk * a.Sk * (2 * D), a.v + (int64_t)bk * a.Skc * D,
+  // V codes: the caller's E4M3 V, or its E4M3 copy (dense, Sk keys) when V is E3M2
+  const P3Src src = {a.kbf + (int64_t)bk * a.Sk * (2 * D),
+                     a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
                      a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk};
-  const P3Lane pl = p3_lane<D>(wave, lane);
+  const P3Lane pl = p3_lane<D, NW>(wave, lane);
   const float c = SOFTCAP ? 1.0f : in_vgpr(a.c_log2);
 
   v16f o[D / 32];
@@ -1617,7 +1632,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
         (qw0 + 31 >= a.Sq) || !wave_live);
   };
 
-  if (j0 < j1) p3_dma<D>(src, sKb0, sV0, j0 * BN, wave, pl);
+  if (j0 < j1) p3_dma<D, NW>(src, sKb0, sV0, j0 * BN, wave, pl);
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
   __syncthreads();
 
@@ -1631,7 +1646,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
     // past the last block: keys >= Sk read 0, and nothing reads that stage)
     v16f sc[BN / 32];
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
-    p3_dma<D>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+    p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
     p3_dma_interleave<D>();
     pipe_scores<SOFTCAP>(sc, a);
     if (need_mask(j)) {
@@ -1676,8 +1691,10 @@ __device__ void prefill3_impl(const FaArgs& a) {
   }
 }
 
-#define MXFA_PREFILL3(D, SC, PR, NAME) \
-  extern "C" __global__ void __launch_bounds__(256, 3) NAME(FaArgs a) { prefill3_impl<D, SC, PR>(a); }
+#define MXFA_PREFILL3(D, SC, PR, NAME)                                                           \
+  extern "C" __global__ void __launch_bounds__(64 * P3Waves<D>::N, P3Waves<D>::N == 8 ? 1 : 3) NAME(FaArgs a) { \
+    prefill3_impl<D, SC, PR>(a);                                                                    \
+  }
 MXFA_PREFILL3(64, false, P_R1, mxfa_prefill3_d64)
 MXFA_PREFILL3(128, false, P_R1, mxfa_prefill3_d128)
 MXFA_PREFILL3(64, true, P_R1, mxfa_prefill3_d64_softcap)
@@ -1686,6 +1703,27 @@ MXFA_PREFILL3(64, false, P_R2, mxfa_prefill3_d64_r2)
 MXFA_PREFILL3(128, false, P_R2, mxfa_prefill3_d128_r2)
 MXFA_PREFILL3(64, true, P_R2, mxfa_prefill3_d64_softcap_r2)
 MXFA_PREFILL3(128, true, P_R2, mxfa_prefill3_d128_softcap_r2)
+MXFA_PREFILL3(256, false, P_R1, mxfa_prefill3_d256)
+MXFA_PREFILL3(256, true, P_R1, mxfa_prefill3_d256_softcap)
+MXFA_PREFILL3(256, false, P_R2, mxfa_prefill3_d256_r2)
+MXFA_PREFILL3(256, true, P_R2, mxfa_prefill3_d256_softcap_r2)
+
+// E4M3 copy of E3M2 V (e3m2x4_to_e4m3x4: the same values); one thread per 16 codes.
+// rows = B * Hkv * Sk; row r of the copy is row (r / Sk) * Skc + r % Sk of the cache-strided V.
+extern "C" __global__ void __launch_bounds__(256) mxfa_v_to_e4m3(const uint8_t* __restrict__ v, int64_t rows, int D,
+                                                                  int Sk, int Skc, uint8_t* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // 16-code chunk
+  const int cpr = D / 16;
+  if (c >= rows * cpr) return;
+  const int64_t r = c / cpr;
+  const int col = (int)(c % cpr);
+  const int64_t src = (r / Sk) * Skc + r % Sk;
+  const v4i x = *reinterpret_cast<const v4i*>(v + src * D + col * 16);
+  v4i y;
+#pragma unroll
+  for (int w = 0; w < 4; w++) y[w] = (int)e3m2x4_to_e4m3x4((uint32_t)x[w]);
+  *reinterpret_cast<v4i*>(out + r * D + col * 16) = y;
+}
 
 
 // ---------------------------------------------------------------------------

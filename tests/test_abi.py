@@ -33,7 +33,8 @@ def test_code_object_present_and_for_gfx950():
     assert b"gfx950" in data
     for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows",
               "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2", "mxfa_decode_scratch", "mxfa_k_to_bf16",
-              "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill_pipe_d128"):
+              "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill_pipe_d128", "mxfa_prefill3_d256_softcap",
+              "mxfa_v_to_e4m3"):
         assert k.encode() in data
 
 
@@ -166,15 +167,15 @@ def test_decode_noalloc_rejects_before_touching_the_device():
 
 
 def test_prefill_plan_and_workspace_checks():
-    """mxfa_prefill_plan: the bf16 K copy (B * Hkv * Sk * D * 2 bytes) for D <= 128 with E4M3 V,
-    0 for D = 256 or E3M2 V; mxfa_prefill_ws rejects a missing or short workspace with
-    MXFA_ERR_WORKSPACE before touching the device."""
+    """mxfa_prefill_plan: the bf16 K copy (B * Hkv * Sk * D * 2 bytes), plus the E4M3 copy of
+    an E3M2 V (B * Hkv * Sk * D bytes); mxfa_prefill_ws rejects a missing or short workspace
+    with MXFA_ERR_WORKSPACE before touching the device."""
     L = mxfa.lib()
     p = mxfa.make_params(2, 32, 8, 4096, 4096, 128, causal=True)
     assert mxfa.prefill_plan(p) == 2 * 8 * 4096 * 128 * 2
     assert mxfa.prefill_plan(mxfa.make_params(1, 4, 2, 64, 4096, 64, kv_stride=8192)) == 2 * 4096 * 64 * 2
-    assert mxfa.prefill_plan(mxfa.make_params(1, 16, 8, 128, 128, 256)) == 0
-    assert mxfa.prefill_plan(mxfa.make_params(1, 4, 2, 64, 64, 128, v_fmt=mxfa.FMT_E3M2)) == 0
+    assert mxfa.prefill_plan(mxfa.make_params(1, 16, 8, 128, 128, 256)) == 8 * 128 * 256 * 2
+    assert mxfa.prefill_plan(mxfa.make_params(1, 4, 2, 64, 64, 128, v_fmt=mxfa.FMT_E3M2)) == 2 * 64 * 128 * 3
     assert L.mxfa_prefill_plan(ctypes.byref(p), None) == 1
     assert L.mxfa_prefill_plan(ctypes.byref(mxfa.make_params(1, 3, 2, 32, 64, 64)), ctypes.byref(ctypes.c_size_t())) == 1
     buf = (ctypes.c_uint8 * 64)()

@@ -30,11 +30,14 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
                          v_fmt=v_fmt, p_rule=p_rule)
     out = torch.full((B, Hq, Sq, D), float("nan"), dtype=torch.float32, device=DEV)
     mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
-    # the workspace-free kernel (mxfa_prefill) runs the same arithmetic in the same order
+    # the workspace-free kernel (mxfa_prefill): for D <= 128 with E4M3 V the same arithmetic in
+    # the same order (bit-identical O); otherwise the staged kernel, checked against the oracle
     out_nw = torch.full_like(out, float("nan"))
     mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out_nw, workspace=False)
     torch.cuda.synchronize()
-    assert torch.equal(out, out_nw), "mxfa_prefill_ws and mxfa_prefill differ"
+    same_kernel_order = D <= 128 and v_fmt == mxfa.FMT_E4M3
+    if same_kernel_order:
+        assert torch.equal(out, out_nw), "mxfa_prefill_ws and mxfa_prefill differ"
     o = np_(out)
     assert np.all(np.isfinite(o)), "coverage: some O elements were not written"
     want = O.attention(oracle_params(p), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
@@ -46,6 +49,14 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
     rel, mab = errors(o, want)
     print(f"   rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
     assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+    if not same_kernel_order:
+        o2 = np_(out_nw)
+        assert np.all(np.isfinite(o2))
+        if heads is not None:
+            o2 = o2.reshape(B * Hq, Sq, D)[idx]
+        rel2, mab2 = errors(o2, want)
+        print(f"   workspace-free kernel: rel-L2 {rel2:.3e} max-abs {mab2:.3e}", flush=True)
+        assert rel2 <= REL_L2_TOL and mab2 <= MAX_ABS_TOL
     return p, dev, out
 
 
