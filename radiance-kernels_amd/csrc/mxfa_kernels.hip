@@ -1194,17 +1194,26 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
   l = l * corr + ((part[0] + part[1]) + (part[2] + part[3]));
 }
 // Score post-processing of one block in place: softcap (log2 units), then the mask.
-template <bool SOFTCAP>
+// softcap * tanh(u), u = s * scale / softcap, in log2 units: cap_log2 * (1 - 2 / (e + 1)) with
+// e = exp2(2 log2(e) u) -- an exponential, a reciprocal and a multiply-add per score; e = inf
+// and e = 0 give +-cap_log2 exactly.
+// VG: the three constants in VGPRs (full-rate VALU at three waves per SIMD; at two waves an
+// SGPR operand costs nothing and saves the registers).
+template <bool SOFTCAP, bool VG = true>
 __device__ __forceinline__ void pipe_scores(v16f (&s)[BN / 32], const FaArgs& a) {
   if (SOFTCAP) {
+    float k2 = 2.0f * LOG2E_F * a.sc_u, cap = a.cap_log2, cap2 = -2.0f * a.cap_log2;
+    if (VG) {
+      k2 = in_vgpr(k2);
+      cap = in_vgpr(cap);
+      cap2 = in_vgpr(cap2);
+    }
 #pragma unroll
     for (int t = 0; t < BN / 32; t++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float u = s[t][i] * a.sc_u;
-        const float e = __builtin_amdgcn_exp2f(-2.0f * LOG2E_F * fabsf(u));
-        const float th = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
-        s[t][i] = a.cap_log2 * (u < 0.0f ? -th : th);
+        const float e = __builtin_amdgcn_exp2f(s[t][i] * k2);
+        s[t][i] = __builtin_fmaf(cap2, __builtin_amdgcn_rcpf(e + 1.0f), cap);
       }
   }
 }
@@ -1254,6 +1263,40 @@ __device__ __forceinline__ void pipe_pv(v16f (&o)[D / 32], const PvRegs<D>& pr, 
   const int pscale = psc[lane >> 5];
 #pragma unroll
   for (int dt = 0; dt < D / 32; dt++) o[dt] = mfma_mx(pr.va[dt], pb, o[dt], pr.vs[dt], pscale);
+}
+
+// PV of one block in NP parts of D / NP columns: the operand registers of one part at a time
+// (D = 256 at two waves per SIMD: 32 registers instead of 64).
+template <int D, int NP>
+__device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, const v8i& pb, const int (&psc)[BN / 32],
+                                         int lane) {
+  constexpr int NT = D / 32 / NP;
+  const int r = lane & 31, h = lane >> 5;
+  const int l16 = lane & 15, g16 = lane >> 4;
+  const int t8 = l16 >> 1;
+  const int kl = 8 * (t8 >> 2) + 4 * h + (t8 & 3);
+  const int sg = (g16 & 1) ^ vsw<D>(kl);
+  const int pscale = psc[lane >> 5];
+#pragma unroll
+  for (int part = 0; part < NP; part++) {
+    v8i va[NT];
+    int vs[NT];
+#pragma unroll
+    for (int u = 0; u < NT; u++) {
+      const int dt = part * NT + u;
+      const uint8_t* base = sv + kl * D + (((2 * dt) ^ sg) << 4) + 8 * (l16 & 1);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + (32 * (q >> 1) + 16 * (q & 1)) * D));
+        va[u][2 * q] = rv[0];
+        va[u][2 * q + 1] = rv[1];
+      }
+      vs[u] = sv[PipeLds<D>::V + h * D + dt * 32 + r];
+    }
+#pragma unroll
+    for (int u = 0; u < NT; u++) o[part * NT + u] = mfma_mx(va[u], pb, o[part * NT + u], vs[u], pscale);
+    if (part + 1 < NP) __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 template <int D, bool SOFTCAP, int PR>
@@ -1618,7 +1661,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
                      a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
                      a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk};
   const P3Lane pl = p3_lane<D, NW>(wave, lane);
-  const float c = SOFTCAP ? 1.0f : in_vgpr(a.c_log2);
+  const float c = SOFTCAP ? 1.0f : (NW == 4 ? in_vgpr(a.c_log2) : a.c_log2);
 
   v16f o[D / 32];
 #pragma unroll
@@ -1648,7 +1691,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
     p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
     p3_dma_interleave<D>();
-    pipe_scores<SOFTCAP>(sc, a);
+    pipe_scores<SOFTCAP, NW == 4>(sc, a);
     if (need_mask(j)) {
       const int ln = fresh_lane();
       int klo, khi;
@@ -1665,9 +1708,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
 #pragma unroll
         for (int i = 0; i < 16; i++) o[dt][i] *= corr;
     }
-    PvRegs<D> pr;
-    pipe_pv_load<D>(pr, v_cur, fresh_lane());
-    pipe_pv<D>(o, pr, pb, psc, lane);
+    pv_parts<D, D == 256 ? 2 : 1>(o, v_cur, pb, psc, fresh_lane());
     __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);   // vmcnt(0) lgkmcnt(0): next stage landed
     __builtin_amdgcn_s_barrier();
   };
