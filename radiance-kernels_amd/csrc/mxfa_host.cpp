@@ -433,8 +433,8 @@ mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p
 }  // extern "C"
 
 namespace {
-// Workgroup shape of the prefill kernels: nw waves (4, or 8 for the D = 256 workspace
-// kernel), hpw query heads (of one KV head) per workgroup, nw / hpw 32-query waves each.
+// Workgroup shape of the prefill kernels: nw waves, hpw query heads (of one KV head) per
+// workgroup, nw / hpw 32-query waves each.
 FaArgs prefill_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
                     const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, int nw, dim3& grid) {
   FaArgs a = make_args(p, q, q_sc, k, k_sc, v, v_sc, o);
@@ -451,7 +451,7 @@ FaArgs prefill_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* 
 }
 
 // Waves per workgroup of the workspace kernel (mxfa_prefill3_*).
-int prefill3_waves(const mxfa_attn_params* p) { return p->head_dim == 256 ? 8 : 4; }
+int prefill3_waves(const mxfa_attn_params*) { return 4; }
 
 // Workspace of mxfa_prefill_ws: the bf16 copy of K, then (E3M2 V) the E4M3 copy of V.
 size_t prefill3_kbf_bytes(const mxfa_attn_params* p) {

@@ -1513,32 +1513,38 @@ template <int D> struct P3Lds {
   static constexpr int SCB = 2 * D > 256 ? 2 * D : 256;   // V scales [BN / 32][D], dword DMA
 };
 
-// Waves per prefill3 workgroup: 4 (three workgroups per CU) for D <= 128; 8 for D = 256,
-// whose double-buffered tiles (97 KB) allow one workgroup per CU -- two waves per SIMD.
-template <int D> struct P3Waves { static constexpr int N = D == 256 ? 8 : 4; };
+// Waves per prefill3 workgroup (4) and K stages: two for D <= 128 (three workgroups per CU);
+// one for D = 256 (65 KB of tiles: two independent workgroups per CU, two waves per SIMD),
+// whose next K block is brought in after every wave has read the current one.
+template <int D> struct P3Waves { static constexpr int N = 4; };
+template <int D> constexpr bool p3_one_k_stage() { return D == 256; }
 
 // DMA of one key block into the prefill3 tiles by NW waves.  K: the four 16-row groups of the
 // chunk-major tile, NW / 4 waves per group, each issuing 2D / 64 / (NW / 4) instructions of
 // four 16-byte chunks per row (wave-uniform column offset as the scalar offset, within a
 // row, so the range check sees the row either way).  V: VDMA / NW instructions per wave
-// whose rows share the swizzle bits (D = 128: i0 = 4(w / 2) + w % 2 and i0 + 2; D = 256:
-// 2w and 2w + 1; D = 64: w).  V scales: every wave issues the same dword instructions (same
-// bytes), so the sequence has no branch.  Per block the buffer resources start at the
-// block and end at key Sk (keys >= Sk read 0); the vector offsets are loop-invariant.
+// whose rows share the swizzle bits (p3_v_instr).  V scales: every wave issues the same dword
+// instructions (same bytes), so the sequence has no branch.  Per block the buffer resources
+// start at the block and end at key Sk (keys >= Sk read 0); the vector offsets are
+// loop-invariant.
 struct P3Lane {
   int k, v, s;
 };
 
-template <int D> __device__ __forceinline__ int p3_v_i0(int wave) {
-  if constexpr (D == 256) return 2 * wave;
-  return D == 128 ? 4 * (wave >> 1) + (wave & 1) : wave;
+// V DMA instruction m of wave w (1024 / D rows each).  The swizzle uses key bits 1 and 3
+// (D = 128: instructions of equal parity), bits 0, 1, 3 (D = 256: equal bit 1) or bits 0
+// and 3 (D = 64: within one instruction).
+template <int D, int NW> __device__ __forceinline__ int p3_v_instr(int w, int m) {
+  if constexpr (D == 128) return 4 * (w >> 1) + (w & 1) + 2 * m;                       // NW = 4
+  else if constexpr (D == 256 && NW == 8) return 2 * w + m;
+  else if constexpr (D == 256) return 2 * (w & 1) + 8 * (w >> 1) + (m & 1) + 4 * (m >> 1);   // NW = 4
+  else return w + 4 * m;                                                                  // D = 64
 }
-template <int D> constexpr int p3_v_step() { return D == 128 ? 2 : 1; }   // between a wave's V instructions
 
 template <int D, int NW> __device__ __forceinline__ P3Lane p3_lane(int wave, int lane) {
   constexpr unsigned VRPI = 1024 / D, CPR = D / 16, WPG = NW / 4, IPW = 2 * D / 64 / WPG;
   const unsigned ln = (unsigned)lane, w = (unsigned)wave;
-  const unsigned vrow = (unsigned)p3_v_i0<D>(wave) * VRPI + ln / CPR, pos = ln % CPR;
+  const unsigned vrow = (unsigned)p3_v_instr<D, NW>(wave, 0) * VRPI + ln / CPR, pos = ln % CPR;
   return {(int)((16 * (w / WPG) + ln % 16) * (2 * D) + (w % WPG) * IPW * 64 + (ln / 16) * 16),
           (int)(vrow * D + ((pos ^ (unsigned)vsw<D>((int)vrow)) << 4)), (int)(ln * 4)};
 }
@@ -1563,10 +1569,12 @@ __device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v
   }
   if constexpr (DO_V) {
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(src.v, (int64_t)key0 * D, (int64_t)(src.Sk - key0) * D);
-    const int i0 = p3_v_i0<D>(wave);
+    const int i0 = p3_v_instr<D, NW>(wave, 0);
 #pragma unroll
-    for (int m = 0; m < VPW; m++)
-      dma_lds<16>(rv, v + (i0 + m * p3_v_step<D>()) * 1024, pl.v + m * p3_v_step<D>() * 1024);
+    for (int m = 0; m < VPW; m++) {
+      const int i = p3_v_instr<D, NW>(wave, m);
+      dma_lds<16>(rv, v + i * 1024, pl.v + (i - i0) * 1024);
+    }
     const int off = (key0 / 32) * D;
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src.vs, off, (int64_t)(src.Sk / 32) * D - off);
 #pragma unroll
@@ -1616,8 +1624,9 @@ __device__ void prefill3_impl(const FaArgs& a) {
   using L = P3Lds<D>;
   constexpr int NW = P3Waves<D>::N;
   fp32_flush_denormals();   // pipe_softmax's R1 flush
+  constexpr bool K1 = p3_one_k_stage<D>();
   __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
-  __shared__ __attribute__((aligned(16))) uint8_t sKb1[L::KB];
+  __shared__ __attribute__((aligned(16))) uint8_t sKb1[K1 ? 16 : L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sV0[L::V + L::SCB];
   __shared__ __attribute__((aligned(16))) uint8_t sV1[L::V + L::SCB];
 
@@ -1681,16 +1690,23 @@ __device__ void prefill3_impl(const FaArgs& a) {
 
   auto step = [&](auto stc, int j) {
     constexpr int ST = decltype(stc)::value;
-    uint8_t* kb_cur = ST ? sKb1 : sKb0;
-    uint8_t* kb_dma = ST ? sKb0 : sKb1;
+    uint8_t* kb_cur = K1 || !ST ? sKb0 : sKb1;
+    uint8_t* kb_dma = K1 || ST ? sKb0 : sKb1;
     uint8_t* v_cur = ST ? sV1 : sV0;
     uint8_t* v_dma = ST ? sV0 : sV1;
-    // the DMA instructions of block j+1 are issued between the score MFMAs of block j (also
-    // past the last block: keys >= Sk read 0, and nothing reads that stage)
+    // the DMA instructions of block j+1 (also past the last block: keys >= Sk read 0, and
+    // nothing reads that stage) are issued between the score MFMAs of block j, or -- one K
+    // stage -- once every wave has read K(j), while the MFMAs run
     v16f sc[BN / 32];
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
-    p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
-    p3_dma_interleave<D>();
+    if constexpr (K1) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's K operand reads are done
+      __builtin_amdgcn_s_barrier();
+      p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+    } else {
+      p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+      p3_dma_interleave<D>();
+    }
     pipe_scores<SOFTCAP, NW == 4>(sc, a);
     if (need_mask(j)) {
       const int ln = fresh_lane();
@@ -1733,7 +1749,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
 }
 
 #define MXFA_PREFILL3(D, SC, PR, NAME)                                                           \
-  extern "C" __global__ void __launch_bounds__(64 * P3Waves<D>::N, P3Waves<D>::N == 8 ? 1 : 3) NAME(FaArgs a) { \
+  extern "C" __global__ void __launch_bounds__(64 * P3Waves<D>::N, p3_one_k_stage<D>() ? 2 : 3) NAME(FaArgs a) { \
     prefill3_impl<D, SC, PR>(a);                                                                    \
   }
 MXFA_PREFILL3(64, false, P_R1, mxfa_prefill3_d64)
