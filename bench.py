@@ -143,6 +143,22 @@ def measured_traffic():
     return None
 
 
+COUNTERS_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_counters.txt")
+
+
+def measured_mfma_busy():
+    """MFMA-busy % of the configs[2] attention kernel from the committed rocprofv3 --pmc summary
+    (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES x 1024 SIMDs), or None."""
+    try:
+        with open(COUNTERS_PROFILE) as f:
+            for line in f:
+                if line.startswith("mfma_busy_pct:"):
+                    return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def calibrate_copy(torch):
     """A plain device-to-device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
     counters (run under rocprofv3 --pmc)."""
@@ -352,6 +368,8 @@ def main():
         "pct_mxfp8_peak": round(100.0 * tflops / MXFP8_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic()},
+        "mfma_busy": {"pct": measured_mfma_busy(), "source": "profiles/prefill_c3_counters.txt",
+                      "kernel": "mxfa_prefill3_d128"},
     }
 
     # the same workload with the reference device kernels' P rule (R2 compatibility mode)
