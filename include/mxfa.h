@@ -138,6 +138,25 @@ mxfa_status mxfa_prefill_ws(const mxfa_attn_params *p,
                             const uint8_t *v, const uint8_t *v_sc,
                             float *o, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Test entry: the stages of the workspace prefill for query rows 32 * q_tile .. + 31 of head bh
+ * (= batch * num_q_heads + query head), as its own routines compute them.  Runs the one
+ * workgroup of mxfa_prefill_ws that holds those rows (writing their O rows, bit-identical to
+ * mxfa_prefill_ws) and records, for each key block the workgroup processes:
+ *   s_out  [32][seq_k]        scores after softcap and mask (-inf masked); units: the raw
+ *                             dot product q.k without softcap, softcap * tanh(.) * log2(e) with
+ *   ml_out [ceil(seq_k/64)][32][2]  running max (same units) and row sum after the block
+ *   p_out  [32][seq_k]        P codes (E4M3), ps_out [32][seq_k / 32] their E8M0 scale codes.
+ * Entries of blocks the workgroup skips (outside the causal / window range) are not written.
+ * Mirrors the reference's stage goldens (kernels/flash_attention_mx/fa_gen_goldens.py:52-58:
+ * S, m, l, P codes and scales). */
+mxfa_status mxfa_prefill_trace(const mxfa_attn_params *p,
+                               const uint8_t *q, const uint8_t *q_sc,
+                               const uint8_t *k, const uint8_t *k_sc,
+                               const uint8_t *v, const uint8_t *v_sc,
+                               float *o, void *workspace, size_t workspace_bytes,
+                               int32_t bh, int32_t q_tile, float *s_out, float *ml_out,
+                               uint8_t *p_out, uint8_t *ps_out, void *stream);
+
 /* Split-KV decode plan for seq_q == 1 (q_pos0 is the query's position, normally
  * seq_k - 1): the 64-key blocks are dealt to *n_parts independent partials (partial i
  * takes blocks i, i + n_parts, ...; each a streaming pass) merged in order by

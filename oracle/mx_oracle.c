@@ -271,9 +271,28 @@ static double score_of(const orc_attn_params *p, const double *qd, const double 
  * Outputs unnormalized O, running max m and sum l. */
 /* One streaming pass over the key blocks starting at k0, k0 + stride, ... below k1; each
  * block is [b0, min(b0 + block_n, k1)).  stride = block_n: the keys [k0, k1) in order. */
+/* Stage record of one row's pass (orc_attention_trace): per key the score S (natural units,
+ * -inf where masked) and the P code, per 32-key group the P scale code, per block the running
+ * (m, l) after it.  NULL members are not written. */
+typedef struct {
+  float *S;
+  uint8_t *codes, *scales;
+  double *ml;
+} orc_trace_t;
+
+static void flash_pass_tr(const orc_attn_params *p, const double *qd, const double *kd, const double *vd,
+                          int64_t qpos, int64_t k0, int64_t k1, int block_n, int64_t stride,
+                          double *O, double *m_out, double *l_out, double *S, float *P, const orc_trace_t *tr);
+
 static void flash_pass(const orc_attn_params *p, const double *qd, const double *kd, const double *vd,
                        int64_t qpos, int64_t k0, int64_t k1, int block_n, int64_t stride,
                        double *O, double *m_out, double *l_out, double *S, float *P) {
+  flash_pass_tr(p, qd, kd, vd, qpos, k0, k1, block_n, stride, O, m_out, l_out, S, P, NULL);
+}
+
+static void flash_pass_tr(const orc_attn_params *p, const double *qd, const double *kd, const double *vd,
+                          int64_t qpos, int64_t k0, int64_t k1, int block_n, int64_t stride,
+                          double *O, double *m_out, double *l_out, double *S, float *P, const orc_trace_t *tr) {
   int D = p->head_dim;
   double m = -INFINITY, l = 0.0;
   for (int d = 0; d < D; d++) O[d] = 0.0;
@@ -287,7 +306,14 @@ static void flash_pass(const orc_attn_params *p, const double *qd, const double 
       if (S[t] > bmax) bmax = S[t];
     }
     double m_new = m > bmax ? m : bmax;
-    if (m_new == -INFINITY) continue;               /* nothing visible yet */
+    if (tr && tr->S)
+      for (int t = 0; t < n; t++) tr->S[b0 + t] = (float)S[t];
+    if (m_new == -INFINITY) {                       /* nothing visible yet */
+      if (tr && tr->ml) { tr->ml[2 * (b0 / block_n)] = -INFINITY; tr->ml[2 * (b0 / block_n) + 1] = 0.0; }
+      if (tr && tr->codes)
+        for (int t = 0; t < n; t++) tr->codes[b0 + t] = 0;
+      continue;
+    }
     double corr = (m == -INFINITY) ? 0.0 : exp(m - m_new);
     for (int t = 0; t < n; t++) P[t] = S[t] == -INFINITY ? 0.0f : (float)exp(S[t] - m_new);
     /* requant P per 32-key group (global key index): rule R1 E4M3, or rule R2 on the
@@ -301,6 +327,12 @@ static void flash_pass(const orc_attn_params *p, const double *qd, const double 
     double lsum = 0.0;
     for (int t = 0; t < n; t++) lsum += (double)P[t];
     l = l * corr + lsum;
+    if (tr) {
+      if (tr->codes) memcpy(tr->codes + b0, gcodes, (size_t)n);
+      if (tr->scales)
+        for (int t = 0; t < n; t += 32) tr->scales[(b0 + t) / 32] = gsc[t / 32];
+      if (tr->ml) { tr->ml[2 * (b0 / block_n)] = m_new; tr->ml[2 * (b0 / block_n) + 1] = l; }
+    }
     for (int d = 0; d < D; d++) O[d] *= corr;
     for (int t = 0; t < n; t += 32) {
       int g = n - t < 32 ? n - t : 32;
@@ -455,6 +487,39 @@ int orc_attention(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_s
                   float *o, int block_n, int split_len, int n_parts, const int32_t *heads, int nheads,
                   int nthreads) {
   return run_attention(p, q, q_sc, k, k_sc, v, v_sc, o, block_n, split_len, n_parts, 0, heads, nheads, nthreads);
+}
+
+/* The stages of one query row's single streaming pass (the prefill schedule: key blocks of
+ * block_n in order): S [seq_k] (natural units after scale, softcap and mask), P codes
+ * [seq_k], P scale codes [seq_k / 32], (m, l) after each block [ceil(seq_k / block_n)][2].
+ * Returns 0, or -1 on invalid arguments. */
+int orc_attention_trace(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,
+                        const uint8_t *k, const uint8_t *k_sc, const uint8_t *v, const uint8_t *v_sc,
+                        int block_n, int64_t bh, int64_t qi, float *S_out, uint8_t *codes_out,
+                        uint8_t *scales_out, double *ml_out) {
+  if (!p || p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0 || p->seq_q <= 0 ||
+      p->seq_k <= 0 || p->head_dim <= 0 || p->head_dim % 32 || p->seq_k % 32 ||
+      p->num_q_heads % p->num_kv_heads)
+    return -1;
+  if (block_n <= 0 || block_n % 32 || block_n > ORC_MAX_BLOCK_N) return -1;
+  if (p->p_rule != ORC_P_R1 && p->p_rule != ORC_P_R2) return -1;
+  if (bh < 0 || bh >= (int64_t)p->batch * p->num_q_heads || qi < 0 || qi >= p->seq_q) return -1;
+  int64_t D = p->head_dim, nb = D / 32, Sk = p->seq_k;
+  int64_t b = bh / p->num_q_heads, h = bh % p->num_q_heads;
+  int64_t kvh = b * p->num_kv_heads + h / (p->num_q_heads / p->num_kv_heads);
+  double *kd = malloc(sizeof(double) * Sk * D), *vd = malloc(sizeof(double) * Sk * D);
+  double *qd = malloc(sizeof(double) * D), *O = malloc(sizeof(double) * D);
+  int64_t sl = Sk > block_n ? Sk : block_n;
+  double *S = malloc(sizeof(double) * sl);
+  float *P = malloc(sizeof(float) * sl);
+  dequant_kv(p, k, k_sc, v, v_sc, kvh, kd, vd);
+  const uint8_t *qc = q + (bh * p->seq_q + qi) * D, *qs = q_sc + (bh * p->seq_q + qi) * nb;
+  for (int64_t d = 0; d < D; d++) qd[d] = orc_decode_elem(qc[d], ORC_FMT_E4M3) * orc_e8m0_decode(qs[d / 32]);
+  orc_trace_t tr = {S_out, codes_out, scales_out, ml_out};
+  double m, l;
+  flash_pass_tr(p, qd, kd, vd, p->q_pos0 + qi, 0, Sk, block_n, block_n, O, &m, &l, S, P, &tr);
+  free(kd); free(vd); free(qd); free(O); free(S); free(P);
+  return 0;
 }
 
 int orc_attention_dense(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,

@@ -27,6 +27,13 @@ struct FaArgs {
   float c_log2;       // softmax_scale * log2(e)  (no softcap)
   float sc_u;         // softmax_scale / softcap
   float cap_log2;     // softcap * log2(e) (0 = no softcap)
+  // stage trace (mxfa_prefill_trace): the workgroup of item (tr_qx, tr_qy) runs alone and the
+  // wave holding query rows tr_q0 .. tr_q0 + 31 of head tr_head records its stages
+  float* tr_s;        // [32][Sk] scores after softcap and mask (kernel units)
+  float* tr_ml;       // [n_blocks][32][2] (m, l) after each block (kernel units; l summed over the row)
+  uint8_t* tr_p;      // [32][Sk] P codes
+  uint8_t* tr_ps;     // [32][Sk / 32] P scale codes
+  int tr_head, tr_q0, tr_qx, tr_qy;
 };
 
 // Size of the code object's device-resident decode scratch (mxfa_decode_scratch), the partials

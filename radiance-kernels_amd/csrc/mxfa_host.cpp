@@ -55,6 +55,10 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3_d128_softcap_r2",
     "mxfa_prefill3_d256",      "mxfa_prefill3_d256_softcap", "mxfa_prefill3_d256_r2", "mxfa_prefill3_d256_softcap_r2",
     "mxfa_v_to_e4m3",
+    "mxfa_prefill3_trace_d64", "mxfa_prefill3_trace_d128", "mxfa_prefill3_trace_d256",
+    "mxfa_prefill3_trace_d64_softcap", "mxfa_prefill3_trace_d128_softcap", "mxfa_prefill3_trace_d256_softcap",
+    "mxfa_prefill3_trace_d64_r2", "mxfa_prefill3_trace_d128_r2", "mxfa_prefill3_trace_d256_r2",
+    "mxfa_prefill3_trace_d64_softcap_r2", "mxfa_prefill3_trace_d128_softcap_r2", "mxfa_prefill3_trace_d256_softcap_r2",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -497,11 +501,20 @@ mxfa_status mxfa_prefill_plan(const mxfa_attn_params* p, size_t* workspace_bytes
   return MXFA_OK;
 }
 
-mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
+}  // extern "C"
+
+namespace {
+// The workspace prefill (mxfa_prefill_ws), or with tr set its stage trace: the one
+// workgroup that holds query rows 32 * tr->q_tile .. + 31 of head tr->bh.
+struct TraceReq {
+  int32_t bh, q_tile;
+  float *s_out, *ml_out;
+  uint8_t *p_out, *ps_out;
+};
+
+mxfa_status prefill_ws_impl(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
                             const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-  if (mxfa_status st = check_params(p, false)) return st;
-  if (prefill_override()) return mxfa_prefill(p, q, q_sc, k, k_sc, v, v_sc, o, stream);
+                            size_t workspace_bytes, void* stream, const TraceReq* tr) {
   const void* ptrs[] = {q, q_sc, k, k_sc, v, v_sc, o};
   if (mxfa_status st = check_ptrs(ptrs, 7)) return st;
   const size_t need = prefill3_workspace(p);
@@ -528,7 +541,43 @@ mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const u
     if (mxfa_status st = launch(dm, "mxfa_v_to_e4m3", cgrid, dim3(256), vargs, stream)) return st;
   }
   void* args[] = {&a};
-  return launch(dm, kernel_name("prefill3", p), grid, dim3((unsigned)(64 * nw)), args, stream);
+  if (!tr) return launch(dm, kernel_name("prefill3", p), grid, dim3((unsigned)(64 * nw)), args, stream);
+  // the item (qx, qy) of the traced rows, as the kernel's own mapping assigns them
+  const int b = tr->bh / p->num_q_heads, head = tr->bh % p->num_q_heads;
+  const int kvh = head / a.group, hc = (head % a.group) / a.hpw;
+  const int qblk = 32 * tr->q_tile / a.qpw;
+  a.tr_qy = (b * p->num_kv_heads + kvh) * (a.group / a.hpw) + hc;
+  a.tr_qx = p->causal ? a.n_qblk - 1 - qblk : qblk;
+  a.tr_head = head;
+  a.tr_q0 = 32 * tr->q_tile;
+  a.tr_s = tr->s_out;
+  a.tr_ml = tr->ml_out;
+  a.tr_p = tr->p_out;
+  a.tr_ps = tr->ps_out;
+  return launch(dm, kernel_name("prefill3_trace", p), dim3(1), dim3((unsigned)(64 * nw)), args, stream);
+}
+}  // namespace
+
+extern "C" {
+
+mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
+                            const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (mxfa_status st = check_params(p, false)) return st;
+  if (prefill_override()) return mxfa_prefill(p, q, q_sc, k, k_sc, v, v_sc, o, stream);
+  return prefill_ws_impl(p, q, q_sc, k, k_sc, v, v_sc, o, workspace, workspace_bytes, stream, nullptr);
+}
+
+mxfa_status mxfa_prefill_trace(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* q_sc, const uint8_t* k,
+                               const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o,
+                               void* workspace, size_t workspace_bytes, int32_t bh, int32_t q_tile, float* s_out,
+                               float* ml_out, uint8_t* p_out, uint8_t* ps_out, void* stream) {
+  if (mxfa_status st = check_params(p, false)) return st;
+  if (bh < 0 || bh >= p->batch * p->num_q_heads || q_tile < 0 || 32 * q_tile >= p->seq_q)
+    return fail(MXFA_ERR_INVALID_ARG, "bh or q_tile out of range");
+  if (!s_out || !ml_out || !p_out || !ps_out) return fail(MXFA_ERR_INVALID_ARG, "NULL trace buffer");
+  const TraceReq tr = {bh, q_tile, s_out, ml_out, p_out, ps_out};
+  return prefill_ws_impl(p, q, q_sc, k, k_sc, v, v_sc, o, workspace, workspace_bytes, stream, &tr);
 }
 
 mxfa_status mxfa_decode_plan(const mxfa_attn_params* p, int32_t* n_parts, size_t* workspace_bytes) {

@@ -1619,7 +1619,7 @@ __device__ __forceinline__ int fresh_lane() {
   return l;
 }
 
-template <int D, bool SOFTCAP, int PR>
+template <int D, bool SOFTCAP, int PR, bool TRACE = false>
 __device__ void prefill3_impl(const FaArgs& a) {
   using L = P3Lds<D>;
   constexpr int NW = P3Waves<D>::N;
@@ -1640,7 +1640,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const int nh_x = cnt_x / a.n_qblk;
   const bool whole_heads = start_x % a.n_qblk == 0 && cnt_x % a.n_qblk == 0;
   const int item = start_x + (whole_heads ? (li % nh_x) * a.n_qblk + li / nh_x : li);
-  const int qx = item % a.n_qblk, qy = item / a.n_qblk;
+  const int qx = TRACE ? a.tr_qx : item % a.n_qblk, qy = TRACE ? a.tr_qy : item / a.n_qblk;
   const int qblk = a.causal ? (a.n_qblk - 1 - qx) : qx;
   const int chunks = a.group / a.hpw;
   const int bk = qy / chunks;
@@ -1652,6 +1652,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const int qi = qw0 + r;
   const bool qvalid = qi < a.Sq;
   const int qpos = a.q_pos0 + qi;
+  const bool traced = TRACE && head == a.tr_head && qw0 == a.tr_q0;   // wave-uniform
 
   const int64_t bh = (int64_t)b * a.Hq + head;
   v4i qb[D / 16];
@@ -1714,10 +1715,41 @@ __device__ void prefill3_impl(const FaArgs& a) {
       key_limits(a, a.q_pos0 + qw0 + (ln & 31), qw0 + (ln & 31) < a.Sq, klo, khi);
       pipe_mask(sc, j * BN, klo, khi, ln >> 5);
     }
+    if constexpr (TRACE) {
+      if (traced) {
+#pragma unroll
+        for (int t = 0; t < BN / 32; t++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const int key = j * BN + 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (key < a.Sk) a.tr_s[(int64_t)r * a.Sk + key] = sc[t][i];
+          }
+      }
+    }
     v8i pb;
     int psc[BN / 32];
     float corr;
     pipe_softmax<SOFTCAP, PR>(m, l, sc, pb, psc, corr, c);
+    if constexpr (TRACE) {
+      const float lrow = pair_sum(l);
+      if (traced) {
+#pragma unroll
+        for (int t = 0; t < BN / 32; t++) {
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int bb = 0; bb < 4; bb++) {
+              const int key = j * BN + 32 * t + 8 * g + 4 * h + bb;
+              if (key < a.Sk) a.tr_p[(int64_t)r * a.Sk + key] = (uint8_t)((uint32_t)pb[4 * t + g] >> (8 * bb));
+            }
+          if (h == 0 && j * BN + 32 * t < a.Sk) a.tr_ps[(int64_t)r * (a.Sk / 32) + (j * BN) / 32 + t] = (uint8_t)psc[t];
+        }
+        if (h == 0) {
+          a.tr_ml[((int64_t)j * 32 + r) * 2] = m;
+          a.tr_ml[((int64_t)j * 32 + r) * 2 + 1] = lrow;
+        }
+      }
+    }
     if (__any(corr != 1.0f)) {
 #pragma unroll
       for (int dt = 0; dt < D / 32; dt++)
@@ -1764,6 +1796,24 @@ MXFA_PREFILL3(256, false, P_R1, mxfa_prefill3_d256)
 MXFA_PREFILL3(256, true, P_R1, mxfa_prefill3_d256_softcap)
 MXFA_PREFILL3(256, false, P_R2, mxfa_prefill3_d256_r2)
 MXFA_PREFILL3(256, true, P_R2, mxfa_prefill3_d256_softcap_r2)
+
+// Stage trace of the same kernel (one workgroup; mxfa_prefill_trace).
+#define MXFA_PREFILL3_TRACE(D, SC, PR, NAME)                                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * P3Waves<D>::N, 1) NAME(FaArgs a) {                        \
+    prefill3_impl<D, SC, PR, true>(a);                                                                        \
+  }
+MXFA_PREFILL3_TRACE(64, false, P_R1, mxfa_prefill3_trace_d64)
+MXFA_PREFILL3_TRACE(128, false, P_R1, mxfa_prefill3_trace_d128)
+MXFA_PREFILL3_TRACE(256, false, P_R1, mxfa_prefill3_trace_d256)
+MXFA_PREFILL3_TRACE(64, true, P_R1, mxfa_prefill3_trace_d64_softcap)
+MXFA_PREFILL3_TRACE(128, true, P_R1, mxfa_prefill3_trace_d128_softcap)
+MXFA_PREFILL3_TRACE(256, true, P_R1, mxfa_prefill3_trace_d256_softcap)
+MXFA_PREFILL3_TRACE(64, false, P_R2, mxfa_prefill3_trace_d64_r2)
+MXFA_PREFILL3_TRACE(128, false, P_R2, mxfa_prefill3_trace_d128_r2)
+MXFA_PREFILL3_TRACE(256, false, P_R2, mxfa_prefill3_trace_d256_r2)
+MXFA_PREFILL3_TRACE(64, true, P_R2, mxfa_prefill3_trace_d64_softcap_r2)
+MXFA_PREFILL3_TRACE(128, true, P_R2, mxfa_prefill3_trace_d128_softcap_r2)
+MXFA_PREFILL3_TRACE(256, true, P_R2, mxfa_prefill3_trace_d256_softcap_r2)
 
 // E4M3 copy of E3M2 V (e3m2x4_to_e4m3x4: the same values); one thread per 16 codes.
 // rows = B * Hkv * Sk; row r of the copy is row (r / Sk) * Skc + r % Sk of the cache-strided V.

@@ -102,7 +102,7 @@ class GemmParams(ctypes.Structure):
 
 
 EXPORTS = ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill", "mxfa_prefill_plan",
-           "mxfa_prefill_ws", "mxfa_decode_plan", "mxfa_decode", "mxfa_decode_noalloc",
+           "mxfa_prefill_ws", "mxfa_prefill_trace", "mxfa_decode_plan", "mxfa_decode", "mxfa_decode_noalloc",
            "mxfa_kv_append", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_shutdown", "mxfa_status_string",
            "mxfa_last_error", "mxfa_version", "mxfa_gemm")
 
@@ -124,6 +124,8 @@ def lib():
         L.mxfa_prefill.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
         L.mxfa_prefill_plan.argtypes = [P(AttnParams), P(ctypes.c_size_t)]
         L.mxfa_prefill_ws.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
+        L.mxfa_prefill_trace.argtypes = ([P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, ctypes.c_int32,
+                                         ctypes.c_int32, f32p, f32p, u8p, u8p, vp])
         L.mxfa_decode_plan.argtypes = [P(AttnParams), P(ctypes.c_int32), P(ctypes.c_size_t)]
         L.mxfa_decode.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp, ctypes.c_size_t, vp]
         L.mxfa_decode_noalloc.argtypes = [P(AttnParams)] + [u8p] * 6 + [f32p, vp]
@@ -137,7 +139,7 @@ def lib():
         L.mxfa_last_error.restype = ctypes.c_char_p
         L.mxfa_version.restype = ctypes.c_int32
         for name in ("mxfa_quantize_rows", "mxfa_quantize_rows_r4", "mxfa_quantize_cols", "mxfa_prefill",
-                     "mxfa_prefill_plan", "mxfa_prefill_ws", "mxfa_decode_plan", "mxfa_decode",
+                     "mxfa_prefill_plan", "mxfa_prefill_ws", "mxfa_prefill_trace", "mxfa_decode_plan", "mxfa_decode",
                      "mxfa_decode_noalloc", "mxfa_softmax_requant", "mxfa_fill_normal", "mxfa_init", "mxfa_kv_append", "mxfa_gemm"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
@@ -273,6 +275,31 @@ def prefill(p, q, qs, k, ks, v, vs, out=None, workspace=None, stream=None):
     _need(workspace, torch.uint8, (workspace.numel(),), "workspace")
     _check(lib().mxfa_prefill_ws(*args, _ptr(workspace), workspace.numel(), _stream(stream)))
     return out
+
+
+def prefill_trace(p, q, qs, k, ks, v, vs, bh, q_tile, stream=None):
+    """Stages of the workspace prefill for query rows 32 * q_tile .. + 31 of head bh
+    (mxfa_prefill_trace): dict of host arrays S [32][Sk] (kernel units, NaN where not
+    written), m and l [n_blocks][32], codes [32][Sk] (0 where not written), scales
+    [32][Sk/32], and the O of the call [B][Hq][Sq][D] (rows of this workgroup only)."""
+    import torch
+    dev = q.device
+    Sk = p.seq_k
+    nblk = (Sk + DEFAULT_BLOCK_N - 1) // DEFAULT_BLOCK_N
+    out = torch.zeros((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device=dev)
+    _check_attn_operands(p, q, qs, k, ks, v, vs, out)
+    ws = torch.empty(max(prefill_plan(p), 16), dtype=torch.uint8, device=dev)
+    s_out = torch.full((32, Sk), float("nan"), dtype=torch.float32, device=dev)
+    ml = torch.full((nblk, 32, 2), float("nan"), dtype=torch.float32, device=dev)
+    codes = torch.zeros((32, Sk), dtype=torch.uint8, device=dev)
+    scales = torch.zeros((32, Sk // 32), dtype=torch.uint8, device=dev)
+    _check(lib().mxfa_prefill_trace(ctypes.byref(p), _ptr(q), _ptr(qs), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs),
+                                    _ptr(out), _ptr(ws), ws.numel(), int(bh), int(q_tile), _ptr(s_out), _ptr(ml),
+                                    _ptr(codes), _ptr(scales), _stream(stream)))
+    torch.cuda.synchronize()
+    mlh = ml.cpu().numpy()
+    return {"S": s_out.cpu().numpy(), "m": mlh[:, :, 0], "l": mlh[:, :, 1], "codes": codes.cpu().numpy(),
+            "scales": scales.cpu().numpy(), "o": out}
 
 
 def decode_plan(p):
