@@ -1276,7 +1276,14 @@ __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, c
   const int t8 = l16 >> 1;
   const int kl = 8 * (t8 >> 2) + 4 * h + (t8 & 3);
   const int sg = (g16 & 1) ^ vsw<D>(kl);
-  const int pscale = psc[lane >> 5];
+  // the lane's row scale of its key half, psc[h], by arithmetic (a select of the two array
+  // elements becomes an indexed load of a private array)
+  const int hmask = -(int)__builtin_amdgcn_ubfe((uint32_t)lane, 5, 1);
+  const int pscale = psc[0] ^ ((psc[0] ^ psc[1]) & hmask);
+  // d tile dt's operand address: the chunk index 2dt ^ sg is 16-byte granular, and the
+  // row offset kl * D sets no bit below 6 (D = 64) or 7 / 8, so over a tile aligned to 256
+  // bytes the LDS address is addr(0) ^ 32 dt
+  const uint32_t a0 = (uint32_t)(uintptr_t)lds_addr(sv) + kl * D + (sg << 4) + 8 * (l16 & 1);
 #pragma unroll
   for (int part = 0; part < NP; part++) {
     v8i va[NT];
@@ -1284,10 +1291,11 @@ __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, c
 #pragma unroll
     for (int u = 0; u < NT; u++) {
       const int dt = part * NT + u;
-      const uint8_t* base = sv + kl * D + (((2 * dt) ^ sg) << 4) + 8 * (l16 & 1);
+      const uint32_t base = a0 ^ (uint32_t)(32 * dt);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + (32 * (q >> 1) + 16 * (q & 1)) * D));
+        const v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i*)(uintptr_t)(base + (32 * (q >> 1) + 16 * (q & 1)) * D));
         va[u][2 * q] = rv[0];
         va[u][2 * q + 1] = rv[1];
       }
@@ -1627,8 +1635,8 @@ __device__ void prefill3_impl(const FaArgs& a) {
   constexpr bool K1 = p3_one_k_stage<D>();
   __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sKb1[K1 ? 16 : L::KB];
-  __shared__ __attribute__((aligned(16))) uint8_t sV0[L::V + L::SCB];
-  __shared__ __attribute__((aligned(16))) uint8_t sV1[L::V + L::SCB];
+  __shared__ __attribute__((aligned(256))) uint8_t sV0[L::V + L::SCB];   // 256-aligned: pv_parts' addresses
+  __shared__ __attribute__((aligned(256))) uint8_t sV1[L::V + L::SCB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
