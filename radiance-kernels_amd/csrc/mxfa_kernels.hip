@@ -1764,7 +1764,8 @@ __device__ void prefill3_impl(const FaArgs& a) {
 #pragma unroll
         for (int i = 0; i < 16; i++) o[dt][i] *= corr;
     }
-    pv_parts<D, D == 256 ? 2 : 1>(o, v_cur, pb, psc, fresh_lane());
+    // D <= 128: the PV addresses stay in registers (loop-invariant); D = 256 has no room
+    pv_parts<D, D == 256 ? 2 : 1>(o, v_cur, pb, psc, D == 256 ? fresh_lane() : lane);
     __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);   // vmcnt(0) lgkmcnt(0): next stage landed
     __builtin_amdgcn_s_barrier();
   };
