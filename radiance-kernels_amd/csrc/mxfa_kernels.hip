@@ -1532,9 +1532,8 @@ template <int D> constexpr bool p3_one_k_stage() { return D == 256; }
 // four 16-byte chunks per row (wave-uniform column offset as the scalar offset, within a
 // row, so the range check sees the row either way).  V: VDMA / NW instructions per wave
 // whose rows share the swizzle bits (p3_v_instr).  V scales: every wave issues the same dword
-// instructions (same bytes), so the sequence has no branch.  Per block the buffer resources
-// start at the block and end at key Sk (keys >= Sk read 0); the vector offsets are
-// loop-invariant.
+// instructions (same bytes), so the sequence has no branch.  The vector offsets are
+// loop-invariant lane parts, the block and column offsets scalar offsets (P3Src).
 struct P3Lane {
   int k, v, s;
 };
@@ -1557,12 +1556,18 @@ template <int D, int NW> __device__ __forceinline__ P3Lane p3_lane(int wave, int
           (int)(vrow * D + ((pos ^ (unsigned)vsw<D>((int)vrow)) << 4)), (int)(ln * 4)};
 }
 
-// Sources of the prefill3 DMA for one (b, KV head): bf16 K rows (2D bytes), V codes
-// (E4M3), V scales.
+// Sources of the prefill3 DMA for one (b, KV head): buffer resources over the bf16 K rows
+// (2D bytes each), the V codes (E4M3) and the V scales, each ending at key Sk.  The block
+// and column offsets go in the loads' scalar offset, which the range check includes (measured
+// on gfx950: a load whose vector offset is in range and whose scalar offset is not reads 0,
+// for plain and LDS-DMA loads alike), so keys >= Sk still read 0.
 struct P3Src {
-  const uint8_t *kbf, *v, *vs;
-  int Sk;
+  __amdgpu_buffer_rsrc_t k, v, vs;
 };
+
+__device__ __forceinline__ P3Src p3_src(const uint8_t* kbf, const uint8_t* v, const uint8_t* vs, int Sk, int D) {
+  return {buf_rsrc(kbf, 0, (int64_t)Sk * (2 * D)), buf_rsrc(v, 0, (int64_t)Sk * D), buf_rsrc(vs, 0, (int64_t)(Sk / 32) * D)};
+}
 
 template <int D, int NW, bool DO_K = true, bool DO_V = true>
 __device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v, int key0, int wave, const P3Lane& pl) {
@@ -1570,23 +1575,19 @@ __device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v
   constexpr int WPG = NW / 4, IPW = 2 * D / 64 / WPG;   // waves per 16-row group, K instructions per wave
   constexpr int VPW = L::VDMA / NW;                     // V instructions per wave
   if constexpr (DO_K) {
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(src.kbf, (int64_t)key0 * (2 * D), (int64_t)(src.Sk - key0) * (2 * D));
     uint8_t* kdst = kb + (wave / WPG) * (32 * D) + (wave % WPG) * IPW * 1024;
 #pragma unroll
-    for (int m = 0; m < IPW; m++) dma_lds<16>(rk, kdst + m * 1024, pl.k, 64 * m);
+    for (int m = 0; m < IPW; m++) dma_lds<16>(src.k, kdst + m * 1024, pl.k, key0 * (2 * D) + 64 * m);
   }
   if constexpr (DO_V) {
-    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(src.v, (int64_t)key0 * D, (int64_t)(src.Sk - key0) * D);
     const int i0 = p3_v_instr<D, NW>(wave, 0);
 #pragma unroll
     for (int m = 0; m < VPW; m++) {
       const int i = p3_v_instr<D, NW>(wave, m);
-      dma_lds<16>(rv, v + i * 1024, pl.v + (i - i0) * 1024);
+      dma_lds<16>(src.v, v + i * 1024, pl.v, key0 * D + (i - i0) * 1024);
     }
-    const int off = (key0 / 32) * D;
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src.vs, off, (int64_t)(src.Sk / 32) * D - off);
 #pragma unroll
-    for (int m = 0; m < (2 * D + 255) / 256; m++) dma_lds<4>(rs, v + L::V + m * 256, pl.s + m * 256);
+    for (int m = 0; m < (2 * D + 255) / 256; m++) dma_lds<4>(src.vs, v + L::V + m * 256, pl.s, (key0 / 32) * D + m * 256);
   }
 }
 
@@ -1675,9 +1676,9 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const bool wave_live = qw0 < a.Sq;
 
   // V codes: the caller's E4M3 V, or its E4M3 copy (dense, Sk keys) when V is E3M2
-  const P3Src src = {a.kbf + (int64_t)bk * a.Sk * (2 * D),
-                     a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
-                     a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk};
+  const P3Src src = p3_src(a.kbf + (int64_t)bk * a.Sk * (2 * D),
+                           a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
+                           a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk, D);
   const P3Lane pl = p3_lane<D, NW>(wave, lane);
   const float c = SOFTCAP ? 1.0f : (NW == 4 ? in_vgpr(a.c_log2) : a.c_log2);
 
