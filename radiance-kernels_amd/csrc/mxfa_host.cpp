@@ -59,6 +59,7 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3_trace_d64_softcap", "mxfa_prefill3_trace_d128_softcap", "mxfa_prefill3_trace_d256_softcap",
     "mxfa_prefill3_trace_d64_r2", "mxfa_prefill3_trace_d128_r2", "mxfa_prefill3_trace_d256_r2",
     "mxfa_prefill3_trace_d64_softcap_r2", "mxfa_prefill3_trace_d128_softcap_r2", "mxfa_prefill3_trace_d256_softcap_r2",
+    "mxfa_gemm_dma",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -413,8 +414,12 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
                                           {"mxfa_gemm_ae3m2", "mxfa_gemm_ae3m2_be3m2"}};
   const int64_t tm = (p->m + 255) / 256, tn = (p->n + 255) / 256;
   g.tiles_n = (int)tn;
-  // the kernels are built for one workgroup size (their launch bounds): 256 or 512 threads
-  const char* name = names[g.a_e3m2][g.b_e3m2];
+  // the kernels are built for one workgroup size (their launch bounds): 256 or 512 threads.
+  // E4M3 operands with whole K steps (k % 128 == 0) take the LDS-DMA kernel
+  // (MXFA_GEMM=reg selects the register-staged one, for comparison).
+  const char* sel = getenv("MXFA_GEMM");
+  const bool dma = !g.a_e3m2 && !g.b_e3m2 && p->k % 128 == 0 && !(sel && std::strcmp(sel, "reg") == 0);
+  const char* name = dma ? "mxfa_gemm_dma" : names[g.a_e3m2][g.b_e3m2];
   int threads = 0;
   MXFA_HIP(hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, fn_by_name(dm, name)));
   if (threads != 256 && threads != 512)

@@ -2545,6 +2545,181 @@ __device__ __forceinline__ void gemm_impl(const GemmArgs& g) {
   }
 }
 
+// MX GEMM with LDS DMA staging (E4M3 x E4M3, K % TK == 0).  The next step's A, B and scale
+// tiles are brought into the other LDS stage by buffer_load ... lds while this step multiplies:
+// no staging registers and no LDS stores by the waves.  A DMA instruction writes 64 lanes x 16
+// bytes contiguously, so the tiles are unpadded and their 16-byte chunks are XOR-swizzled
+// instead (each lane fetches the global chunk that belongs at its LDS position):
+//   A (rows of TK = 128 bytes): chunk c of row r at chunk c ^ ((r >> 1) & 7) -- a ds_read_b128 of
+//     16 consecutive rows at one chunk covers all 64 banks;
+//   B (k rows of 256 bytes): chunk c of row k at chunk c ^ 2 (k & 7) -- the ds_read_b64_tr_b8
+//     reads (8 consecutive k rows x two adjacent chunks per 32 lanes) cover all 64 banks.
+// The scale tile [KB][TM + TN] needs no swizzle (dword DMA, one 256-byte row per instruction).
+template <int NW>
+__device__ __forceinline__ int gemm_dma_swa(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int gemm_dma_swb(int krow) { return 2 * (krow & 7); }
+
+template <int NW>
+__device__ __forceinline__ void gemm_mma_dma(v16f (&acc)[4][GemmCfg<NW>::TJ], const uint8_t* sA, const uint8_t* sB,
+                                             const uint8_t* sS, int wr, int wc, int lane) {
+  using namespace gemm;
+  constexpr int TJ = GemmCfg<NW>::TJ;
+  const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
+  bool first = NW == 8;
+#pragma unroll
+  for (int kh = 0; kh < TK / 64; kh++) {
+    v8i bo[TJ];
+    int bsc[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; j++) {
+      const int ncol = 32 * TJ * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int krow = 64 * kh + 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
+        const int addr = krow * TN + ((((ncol >> 4) ^ gemm_dma_swb(krow))) << 4) + (ncol & 15);
+        v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB + addr));
+        bo[j][2 * q] = t[0];
+        bo[j][2 * q + 1] = t[1];
+      }
+      bsc[j] = sS[KB * TM + (2 * kh + h) * TN + 32 * TJ * wc + 32 * j + r];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = 128 * wr + 32 * i + r;
+      const int sw = gemm_dma_swa<NW>(row);
+      const v4i lo = *reinterpret_cast<const v4i*>(sA + row * TK + (((4 * kh + h) ^ sw) << 4));
+      const v4i hi = *reinterpret_cast<const v4i*>(sA + row * TK + (((4 * kh + 2 + h) ^ sw) << 4));
+      const v8i ao = cat44(lo, hi);
+      const int asc = sS[(2 * kh + h) * TM + row];
+      if (first) {
+        __builtin_amdgcn_s_setprio(1);
+        first = false;
+      }
+#pragma unroll
+      for (int j = 0; j < TJ; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
+    }
+  }
+  if (NW == 8) __builtin_amdgcn_s_setprio(0);
+}
+
+// The DMA of one step into a stage: wave w issues A and B instructions w * IPW .. + IPW - 1
+// (IPW = 32 / NW; instruction i covers A rows 8i .. 8i + 7 and B k rows 4i .. 4i + 3) and one
+// scale row: SA row kb = w % KB (waves < NW / 2) or SB row (the others); with NW = 8 that is
+// every scale row once.
+struct GemmDmaLane {
+  uint32_t a[2], b[2], s;   // vector offsets (A and B by instruction parity: the swizzle alternates)
+};
+
+template <int NW>
+__device__ __forceinline__ void gemm_dma(const GemmArgs& g, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                         __amdgpu_buffer_rsrc_t rs, const GemmDmaLane& dl, uint8_t* sA, uint8_t* sB,
+                                         uint8_t* sS, int wave, int k0) {
+  using namespace gemm;
+  constexpr int IPW = 32 / NW;
+#pragma unroll
+  for (int q = 0; q < IPW; q++) {
+    const int i = wave * IPW + q;
+    dma_lds<16>(ra, sA + i * 1024, dl.a[i & 1], 8 * i * g.K + k0);
+    dma_lds<16>(rb, sB + i * 1024, dl.b[i & 1], (k0 + 4 * i) * g.N);
+  }
+  const bool is_a = wave < NW / 2;
+  const int kb = wave % KB;
+  dma_lds<4>(rs, sS + (is_a ? kb * TM : KB * TM + kb * TN), dl.s, (k0 / 32 + kb) * (is_a ? g.M : g.N));
+}
+
+template <int NW>
+__device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
+  using namespace gemm;
+  using C = GemmCfg<NW>;
+  constexpr int TJ = C::TJ;
+  static_assert(NW == 8, "DMA staging: eight waves (one scale row each)");
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[TM * TK];
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[TM * TK];
+  __shared__ __attribute__((aligned(16))) uint8_t sB0[TK * TN];
+  __shared__ __attribute__((aligned(16))) uint8_t sB1[TK * TN];
+  __shared__ __attribute__((aligned(16))) uint8_t sS0[S_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t sS1[S_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int GM = 4;
+  const int nwg = (int)gridDim.x, lin = (int)blockIdx.x;
+  const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
+  const int item = xcd * per + min(xcd, rem) + (lin >> 3);
+  const int tiles_m = (g.M + TM - 1) / TM;
+  const int group = item / (GM * g.tiles_n), first = group * GM, gm = min(GM, tiles_m - first);
+  const int in_group = item - group * GM * g.tiles_n;
+  const int m0 = (first + in_group % gm) * TM, n0 = (in_group / gm) * TN;
+  const int wr = wave / C::WCN, wc = wave % C::WCN;
+
+  // sources: A rows m0 .. M (rows past M read 0), all of B, SA or SB; the step enters as the
+  // scalar offset
+  const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, 0, (int64_t)g.K * g.N);
+  const bool is_a = wave < NW / 2;
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(is_a ? g.sa : g.sb, 0, (int64_t)(g.K / 32) * (is_a ? g.M : g.N));
+  GemmDmaLane dl;
+#pragma unroll
+  for (int par = 0; par < 2; par++) {
+    // A instruction of parity par: lane row 8i + lane / 8, LDS chunk lane % 8
+    const int ra_row = 8 * par + lane / 8, ca = (lane % 8) ^ gemm_dma_swa<NW>(ra_row);
+    dl.a[par] = (uint32_t)((lane / 8) * g.K + 16 * ca);
+    // B instruction of parity par: lane k row 4i + lane / 16, LDS chunk lane % 16
+    const int kb_row = 4 * par + lane / 16, cb = (lane % 16) ^ gemm_dma_swb(kb_row);
+    dl.b[par] = n0 + 16 * cb < g.N ? (uint32_t)((lane / 16) * g.N + n0 + 16 * cb) : 0x80000000u;
+  }
+  {
+    const int c = (is_a ? m0 : n0) + 4 * lane;
+    dl.s = c < (is_a ? g.M : g.N) ? (uint32_t)c : 0x80000000u;
+  }
+
+  v16f acc[4][TJ];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < TJ; j++) acc[i][j] = (v16f){};
+
+  const int nk = g.K / TK;
+  gemm_dma<NW>(g, ra, rb, rs, dl, sA0, sB0, sS0, wave, 0);
+  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
+  __syncthreads();
+  auto step = [&](auto stc, int kt) {
+    constexpr int ST = decltype(stc)::value;
+    // the next step's tiles into the other stage (the last step reloads itself: in bounds,
+    // never multiplied)
+    gemm_dma<NW>(g, ra, rb, rs, dl, ST ? sA0 : sA1, ST ? sB0 : sB1, ST ? sS0 : sS1, wave, min(kt + 1, nk - 1) * TK);
+    gemm_mma_dma<NW>(acc, ST ? sA1 : sA0, ST ? sB1 : sB0, ST ? sS1 : sS0, wr, wc, lane);
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);   // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < nk) step(std::integral_constant<int, 1>{}, kt + 1);
+  }
+
+  const int r = lane & 31, h = lane >> 5;
+  const int rows = min(TM, g.M - m0);
+  const int ES = g.c_bf16 ? 2 : 4;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.c + (int64_t)m0 * g.N * ES), 0, (int)(uint32_t)((int64_t)rows * g.N * ES), 0x00020000);
+#pragma unroll
+  for (int j = 0; j < TJ; j++) {
+    const int n = n0 + 32 * TJ * wc + 32 * j + r;
+    const uint32_t cb = n < g.N ? (uint32_t)((128 * wr + 4 * h) * g.N + n) * (uint32_t)ES : 0xfffffff0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const uint32_t off = n < g.N ? cb + (uint32_t)((32 * i + 8 * (v >> 2) + (v & 3)) * g.N) * (uint32_t)ES : cb;
+        if (g.c_bf16)
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)acc[i][j][v]), rc, off, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), rc, off, 0, 0);
+      }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_dma(GemmArgs g) { gemm_dma_impl<8>(g); }
+
 // Waves per GEMM workgroup; the host reads the workgroup size from the kernel's
 // launch bounds (its maximum threads per block).
 #ifndef MXFA_GEMM_WAVES
