@@ -132,3 +132,25 @@ def test_gemm_benched_shape_sampled():
     print(f"   sampled rel-L2 {rel_l2(c, want):.2e}, max err / sum|terms| {float((err / ab).max()):.2e}", flush=True)
     assert np.all(err <= ab * 2.0 ** -8 + 1e-38)
     assert rel_l2(c, want) <= 1e-3
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 768, 1024), (272, 528, 512), (8192, 6144, 4096)])
+def test_gemm_dma_kernel_equals_register_staged(monkeypatch, M, N, K):
+    """E4M3 operands with K % 128 == 0 run the LDS-DMA kernel (unpadded XOR-swizzled tiles); the
+    register-staged kernel (MXFA_GEMM=reg) runs the same MFMAs on the same operands in the same
+    order, so C must match bit for bit, fp32 and bf16 -- ragged M and N included."""
+    rng = np.random.default_rng(M + N + K)
+    a, b = _codes(rng, (M, K), 0), _codes(rng, (K, N), 0)
+    sa = rng.integers(112, 142, (K // 32, M)).astype(np.uint8)
+    sb = rng.integers(112, 142, (K // 32, N)).astype(np.uint8)
+    dev = [torch.from_numpy(x).to(DEV) for x in (a, sa, b, sb)]
+    for c_fmt, dt in ((mxfa.C_F32, torch.float32), (mxfa.C_BF16, torch.bfloat16)):
+        outs = []
+        for mode in ("dma", "reg"):
+            monkeypatch.setenv("MXFA_GEMM", mode)
+            c = torch.full((M, N), float("nan"), dtype=dt, device=DEV)
+            mxfa.gemm(*dev, out=c, c_fmt=c_fmt)
+            outs.append(c)
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(outs[0]).all())
+        assert torch.equal(outs[0], outs[1])
