@@ -1137,13 +1137,37 @@ __device__ __forceinline__ uint32_t p_pack4_ftz(float y0, float y1, float y2, fl
   return w ^ (top & ones);                            // 0x7f -> 0x7e, other bytes unchanged
 }
 
+__device__ __forceinline__ float vmin(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float tile_min16(const v16f& x) {
+  float m = vmin(x[0], x[1]);
+#pragma unroll
+  for (int i = 2; i < 16; i++) m = vmin(m, x[i]);
+  return m;
+}
+__device__ __forceinline__ float pair_min_raw(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return vmin(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// With a softcap, s holds r = 1 / (e + 1) per score (pipe_scores; masked keys r = +inf) and
+// the capped score is cap + cap2 * r (cap2 = -2 cap < 0, cap = softcap * log2(e)): the
+// exponent's argument is fma(cap2, r, cap - mu), one operation like fma(s, c, -mu * c)
+// without a softcap.  The score is non-increasing in r (fma rounds monotonically), so the
+// tile maximum is cap + cap2 * min(r), bit for bit the maximum of the capped scores, and
+// -inf for a fully masked tile (cap2 * inf).
 template <bool SOFTCAP, int PR>
 __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 32],
-                                             v8i& pb, int (&psc)[BN / 32], float& corr, float c) {
+                                             v8i& pb, int (&psc)[BN / 32], float& corr, float c,
+                                             float cap2 = 0.0f, float cap = 0.0f) {
   constexpr int NT = BN / 32;
+  if (SOFTCAP) {
+    cap2 = in_vgpr(cap2);
+    cap = in_vgpr(cap);
+  }
   float bmax[NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) bmax[t] = pair_max_raw(tile_max16(s[t]));
+  for (int t = 0; t < NT; t++)
+    bmax[t] = SOFTCAP ? __builtin_fmaf(cap2, pair_min_raw(tile_min16(s[t])), cap) : pair_max_raw(tile_max16(s[t]));
   float rmax = bmax[0];
 #pragma unroll
   for (int t = 1; t < NT; t++) rmax = vmax(rmax, bmax[t]);
@@ -1151,7 +1175,8 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
   const float mu = m_new == -INFINITY ? 0.0f : m_new;
   corr = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mu) * c);
   m = m_new;
-  const float mcn = -(mu * c);
+  const float mcn = SOFTCAP ? cap - mu : -(mu * c);
+  auto arg = [&](float x) { return SOFTCAP ? __builtin_fmaf(cap2, x, mcn) : __builtin_fmaf(x, c, mcn); };
   float part[4];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
@@ -1169,7 +1194,7 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
       float y[16];
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const uint32_t pbits = bf16_rne_bits(__builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], c, mcn)));
+        const uint32_t pbits = bf16_rne_bits(__builtin_amdgcn_exp2f(arg(s[t][i])));
         p[i] = __uint_as_float(pbits);
         y[i] = r2_cut(pbits, bnd);
       }
@@ -1177,7 +1202,7 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
       for (int g = 0; g < 4; g++) w[g] = cvt_pack4(y[4 * g], y[4 * g + 1], y[4 * g + 2], y[4 * g + 3], bnd.scale);
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], c, mcn));
+      for (int i = 0; i < 16; i++) p[i] = __builtin_amdgcn_exp2f(arg(s[t][i]));
       const float f = __uint_as_float((134u - sc) << 23);     // 2^(7 - sc)
       const uint32_t ones = in_vgpr_u(0x01010101u);
 #pragma unroll
@@ -1194,38 +1219,40 @@ __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 
   l = l * corr + ((part[0] + part[1]) + (part[2] + part[3]));
 }
 // Score post-processing of one block in place: softcap (log2 units), then the mask.
-// softcap * tanh(u), u = s * scale / softcap, in log2 units: cap_log2 * (1 - 2 / (e + 1)) with
-// e = exp2(2 log2(e) u) -- an exponential, a reciprocal and a multiply-add per score; e = inf
-// and e = 0 give +-cap_log2 exactly.
-// VG: the three constants in VGPRs (full-rate VALU at three waves per SIMD; at two waves an
-// SGPR operand costs nothing and saves the registers).
+// softcap * tanh(u), u = s * scale / softcap, in log2 units: cap_log2 * (1 - 2 / (e + 1)) =
+// cap_log2 + cap2 * r with e = exp2(2 log2(e) u), r = 1 / (e + 1), cap2 = -2 cap_log2.  s keeps
+// r (an exponential and a reciprocal per score); pipe_softmax applies cap_log2 + cap2 * r
+// inside the exponential's argument.  e = inf and e = 0 give +-cap_log2 exactly.
+// VG: the constant in a VGPR (full-rate VALU at three waves per SIMD; at two waves an SGPR
+// operand costs nothing and saves the register).
 template <bool SOFTCAP, bool VG = true>
 __device__ __forceinline__ void pipe_scores(v16f (&s)[BN / 32], const FaArgs& a) {
   if (SOFTCAP) {
-    float k2 = 2.0f * LOG2E_F * a.sc_u, cap = a.cap_log2, cap2 = -2.0f * a.cap_log2;
-    if (VG) {
-      k2 = in_vgpr(k2);
-      cap = in_vgpr(cap);
-      cap2 = in_vgpr(cap2);
-    }
+    float k2 = 2.0f * LOG2E_F * a.sc_u;
+    if (VG) k2 = in_vgpr(k2);
 #pragma unroll
     for (int t = 0; t < BN / 32; t++)
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const float e = __builtin_amdgcn_exp2f(s[t][i] * k2);
-        s[t][i] = __builtin_fmaf(cap2, __builtin_amdgcn_rcpf(e + 1.0f), cap);
-      }
+      for (int i = 0; i < 16; i++) s[t][i] = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(s[t][i] * k2) + 1.0f);
   }
 }
 
+// The capped score of a softcap block's entry r (for the stage trace).
+__device__ __forceinline__ float capped_score(float r, const FaArgs& a) {
+  return __builtin_fmaf(-2.0f * a.cap_log2, r, a.cap_log2);
+}
+
+// Masked keys get -inf, or with a softcap r = +inf (capped score cap + cap2 * inf = -inf).
+template <bool SOFTCAP>
 __device__ __forceinline__ void pipe_mask(v16f (&s)[BN / 32], int key0, int klo, int khi, int h) {
   const int dhi = khi - key0 - 4 * h, dlo = klo - key0 - 4 * h;
+  constexpr float masked = SOFTCAP ? INFINITY : -INFINITY;
 #pragma unroll
   for (int t = 0; t < BN / 32; t++)
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const int c = 32 * t + 8 * (i >> 2) + (i & 3);
-      s[t][i] = ((c <= dhi) & (c >= dlo)) ? s[t][i] : -INFINITY;
+      s[t][i] = ((c <= dhi) & (c >= dlo)) ? s[t][i] : masked;
     }
 }
 
@@ -1415,7 +1442,7 @@ __device__ void prefill_pipe_impl(const FaArgs& a) {
     pipe_scores<SOFTCAP>(scur, a);
     if (need_mask(j)) {
       __asm__ volatile("");
-      pipe_mask(scur, key0, klo, khi, h);
+      pipe_mask<SOFTCAP>(scur, key0, klo, khi, h);
     }
     // scores of block j+1 (MFMA) with the softmax and requant of block j (VALU); the
     // conversion of K(j+2) and the PV operand reads of block j inside the same region
@@ -1423,7 +1450,7 @@ __device__ void prefill_pipe_impl(const FaArgs& a) {
     v8i pb;
     int psc[BN / 32];
     float corr;
-    pipe_softmax<SOFTCAP, PR>(m, l, scur, pb, psc, corr, c);
+    pipe_softmax<SOFTCAP, PR>(m, l, scur, pb, psc, corr, c, -2.0f * a.cap_log2, a.cap_log2);
     pipe_convert_store<D>(cr, kb_conv, tid);
     PvRegs<D> pr;
     pipe_pv_load<D>(pr, v_cur, lane);
@@ -1722,7 +1749,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
       const int ln = fresh_lane();
       int klo, khi;
       key_limits(a, a.q_pos0 + qw0 + (ln & 31), qw0 + (ln & 31) < a.Sq, klo, khi);
-      pipe_mask(sc, j * BN, klo, khi, ln >> 5);
+      pipe_mask<SOFTCAP>(sc, j * BN, klo, khi, ln >> 5);
     }
     if constexpr (TRACE) {
       if (traced) {
@@ -1731,14 +1758,14 @@ __device__ void prefill3_impl(const FaArgs& a) {
 #pragma unroll
           for (int i = 0; i < 16; i++) {
             const int key = j * BN + 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (key < a.Sk) a.tr_s[(int64_t)r * a.Sk + key] = sc[t][i];
+            if (key < a.Sk) a.tr_s[(int64_t)r * a.Sk + key] = SOFTCAP ? capped_score(sc[t][i], a) : sc[t][i];
           }
       }
     }
     v8i pb;
     int psc[BN / 32];
     float corr;
-    pipe_softmax<SOFTCAP, PR>(m, l, sc, pb, psc, corr, c);
+    pipe_softmax<SOFTCAP, PR>(m, l, sc, pb, psc, corr, c, -2.0f * a.cap_log2, a.cap_log2);
     if constexpr (TRACE) {
       const float lrow = pair_sum(l);
       if (traced) {
