@@ -1735,6 +1735,9 @@ __device__ void prefill3_impl(const FaArgs& a) {
     // nothing reads that stage) are issued between the score MFMAs of block j, or -- one K
     // stage -- once every wave has read K(j), while the MFMAs run
     v16f sc[BN / 32];
+    // the score MFMAs at raised wave priority: the SIMD's arbiter issues them ahead of the
+    // other workgroups' softmax VALU (about 1% faster on the S = 4096 GQA prefill)
+    __builtin_amdgcn_s_setprio(1);
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
     if constexpr (K1) {
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's K operand reads are done
@@ -1744,6 +1747,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
       p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
       p3_dma_interleave<D>();
     }
+    __builtin_amdgcn_s_setprio(0);
     pipe_scores<SOFTCAP, NW == 4>(sc, a);
     if (need_mask(j)) {
       const int ln = fresh_lane();
