@@ -302,6 +302,21 @@ def profile_workload(torch, mxfa, name, args):
                         args.steps, args.warmup, preheat=False)
         print(json.dumps({"profile": name, "ms_per_call": round(ms, 4), "calls": args.steps + args.warmup}), flush=True)
         return
+    elif name == "gemm":
+        M, K, N = 8192, 4096, 6144           # bench_gemm's QKV projection, fp32 C
+        X = torch.empty((M, K), dtype=torch.float32, device=dev)
+        W = torch.empty((K, N), dtype=torch.float32, device=dev)
+        mxfa.fill_normal(X, 41)
+        mxfa.fill_normal(W, 42)
+        xq, xs = mxfa.quantize_rows(X)
+        wq, ws = mxfa.quantize_cols(W)
+        xs = xs.t().contiguous()
+        del X, W
+        c = torch.empty((M, N), dtype=torch.float32, device=dev)
+        ms = time_calls(torch, lambda: mxfa.gemm(xq, xs, wq, ws, out=c), args.steps, args.warmup, preheat=False)
+        print(json.dumps({"profile": name, "ms_per_call": round(ms, 4), "calls": args.steps + args.warmup,
+                          "tflops": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)}), flush=True)
+        return
     else:
         raise SystemExit(f"bench.py: unknown --profile workload {name!r}")
     out = torch.empty((p.batch, p.num_q_heads, p.seq_q, p.head_dim), dtype=torch.float32, device=dev)
@@ -322,7 +337,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="only run a 256 MiB device copy x3")
     ap.add_argument("--profile", metavar="WORKLOAD",
-                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode): W untimed + K timed calls")
+                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode, gemm): W untimed + K timed calls")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in DESIGN.md)",
