@@ -1808,7 +1808,36 @@ __device__ void prefill3_impl(const FaArgs& a) {
 
   const float lt = pair_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if (qvalid) {
+  if constexpr (D >= 128 && !TRACE) {
+    // O through LDS, so that every store instruction writes whole 128-byte lines: a lane of
+    // the MFMA layout holds 16-byte pieces of its row 128 bytes apart, whose line-partial
+    // stores cost 20% extra HBM writes.  Per 64-column chunk the wave writes its 32 x 64
+    // floats to a private 8 KB slice of the K tiles (free after the loop's last barrier; the
+    // 16-byte chunk c of row r at c ^ (r & 15)), then reads 4 rows x 256 contiguous bytes per
+    // instruction and stores them non-temporally (O is not read again here: K and V keep
+    // the L2, 96 -> 68 MB fetched on the S = 4096 GQA prefill).
+    float* const ldsw = reinterpret_cast<float*>(D == 256 ? sKb0 + wave * 8192 : (wave < 2 ? sKb0 : sKb1) + (wave & 1) * 8192);
+#pragma unroll
+    for (int p = 0; p < D / 64; p++) {
+#pragma unroll
+      for (int dd = 0; dd < 2; dd++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int dt = 2 * p + dd, cidx = dd * 8 + 2 * g + h;
+          const float4 w = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                                       o[dt][4 * g + 3] * inv);
+          *reinterpret_cast<float4*>(ldsw + r * 64 + ((cidx ^ (r & 15)) << 2)) = w;
+        }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int row = 4 * k + (lane >> 4), c = lane & 15;
+        const float4 v = *reinterpret_cast<const float4*>(ldsw + row * 64 + ((c ^ (row & 15)) << 2));
+        if (qw0 + row < a.Sq)
+          __builtin_nontemporal_store(__builtin_bit_cast(v4i, v),
+                                      reinterpret_cast<v4i*>(a.o + (bh * a.Sq + qw0 + row) * D + 64 * p + 4 * c));
+      }
+    }
+  } else if (qvalid) {
     float* orow = a.o + (bh * a.Sq + qi) * D;
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++)
