@@ -14,7 +14,7 @@ struct FaArgs {
   float* part_o;      // decode: partial O  [B*Hq][nparts][D]
   float* part_ml;     // decode: partial (m, l) [B*Hq][nparts][2]
   const uint8_t* kbf; // prefill: bf16 copy of K [B][Hkv][Sk][D] (mxfa_k_to_bf16)
-  const uint8_t* vws; // prefill: E4M3 copy of E3M2 V [B][Hkv][Sk][D] (mxfa_v_to_e4m3), else NULL
+  const uint8_t* vws; // prefill: E4M3 copy of E3M2 V [B][Hkv][Sk][D] (mxfa_k_to_bf16), else NULL
   int B, Hq, Hkv, Sq, Sk;
   int Skc;            // keys allocated per (b, KV head) in k/ks/v/vs (>= Sk; base offsets use it)
   int q_pos0, window, causal, v_e3m2;

@@ -54,7 +54,6 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3_d128_softcap", "mxfa_prefill3_d64_r2", "mxfa_prefill3_d128_r2", "mxfa_prefill3_d64_softcap_r2",
     "mxfa_prefill3_d128_softcap_r2",
     "mxfa_prefill3_d256",      "mxfa_prefill3_d256_softcap", "mxfa_prefill3_d256_r2", "mxfa_prefill3_d256_softcap_r2",
-    "mxfa_v_to_e4m3",
     "mxfa_prefill3_trace_d64", "mxfa_prefill3_trace_d128", "mxfa_prefill3_trace_d256",
     "mxfa_prefill3_trace_d64_softcap", "mxfa_prefill3_trace_d128_softcap", "mxfa_prefill3_trace_d256_softcap",
     "mxfa_prefill3_trace_d64_r2", "mxfa_prefill3_trace_d128_r2", "mxfa_prefill3_trace_d256_r2",
@@ -535,16 +534,12 @@ mxfa_status prefill_ws_impl(const mxfa_attn_params* p, const uint8_t* q, const u
   uint8_t* vws = p->v_fmt == MXFA_FMT_E3M2 ? kbf + prefill3_kbf_bytes(p) : nullptr;
   a.kbf = kbf;
   a.vws = vws;
-  // bf16 K (and E4M3 V): one thread per 16 codes
+  // bf16 K (and E4M3 V) in one launch: one thread per 16 codes
   int64_t rows = (int64_t)p->batch * p->num_kv_heads * p->seq_k;
   int D = p->head_dim, Sk = p->seq_k, Skc = a.Skc;
   const dim3 cgrid((unsigned)((rows * (D / 16) + 255) / 256));
-  void* cargs[] = {(void*)&k, (void*)&k_sc, &rows, &D, &Sk, &Skc, &kbf};
+  void* cargs[] = {(void*)&k, (void*)&k_sc, (void*)&v, &rows, &D, &Sk, &Skc, &kbf, &vws};
   if (mxfa_status st = launch(dm, "mxfa_k_to_bf16", cgrid, dim3(256), cargs, stream)) return st;
-  if (vws) {
-    void* vargs[] = {(void*)&v, &rows, &D, &Sk, &Skc, &vws};
-    if (mxfa_status st = launch(dm, "mxfa_v_to_e4m3", cgrid, dim3(256), vargs, stream)) return st;
-  }
   void* args[] = {&a};
   if (!tr) return launch(dm, kernel_name("prefill3", p), grid, dim3((unsigned)(64 * nw)), args, stream);
   // the item (qx, qy) of the traced rows, as the kernel's own mapping assigns them

@@ -33,8 +33,7 @@ def test_code_object_present_and_for_gfx950():
     assert b"gfx950" in data
     for k in ("mxfa_prefill_d128", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows",
               "mxfa_prefill_d128_r2", "mxfa_decode_d64_softcap_r2", "mxfa_decode_scratch", "mxfa_k_to_bf16",
-              "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill_pipe_d128", "mxfa_prefill3_d256_softcap",
-              "mxfa_v_to_e4m3"):
+              "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill_pipe_d128", "mxfa_prefill3_d256_softcap"):
         assert k.encode() in data
 
 
