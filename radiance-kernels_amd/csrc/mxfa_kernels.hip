@@ -1334,6 +1334,39 @@ __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, c
   }
 }
 
+// O of one wave (32 query rows x D, MFMA layout), normalized by inv, stored through LDS so
+// that every store instruction writes whole 128-byte lines: a lane of the MFMA layout holds
+// 16-byte pieces of its row 128 bytes apart, whose line-partial stores cost 20% extra HBM
+// writes.  Per 64-column chunk the wave writes its 32 x 64 floats to its private 8 KB slice
+// ldsw (the 16-byte chunk c of row r at c ^ (r & 15)), then reads 4 rows x 256 contiguous
+// bytes per instruction and stores them non-temporally (O is not read again here, so K and V
+// keep the L2).  Rows qw0 + row >= Sq are not stored.
+template <int D>
+__device__ __forceinline__ void store_o_lds(const v16f (&o)[D / 32], float inv, float* ldsw, float* obase, int qw0,
+                                            int Sq, int lane) {
+  const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int p = 0; p < D / 64; p++) {
+#pragma unroll
+    for (int dd = 0; dd < 2; dd++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int dt = 2 * p + dd, cidx = dd * 8 + 2 * g + h;
+        const float4 w = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                                     o[dt][4 * g + 3] * inv);
+        *reinterpret_cast<float4*>(ldsw + r * 64 + ((cidx ^ (r & 15)) << 2)) = w;
+      }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int row = 4 * k + (lane >> 4), c = lane & 15;
+      const float4 v = *reinterpret_cast<const float4*>(ldsw + row * 64 + ((c ^ (row & 15)) << 2));
+      if (qw0 + row < Sq)
+        __builtin_nontemporal_store(__builtin_bit_cast(v4i, v),
+                                    reinterpret_cast<v4i*>(obase + (int64_t)(qw0 + row) * D + 64 * p + 4 * c));
+    }
+  }
+}
+
 template <int D, bool SOFTCAP, int PR>
 __device__ void prefill_pipe_impl(const FaArgs& a) {
   using L = PipeLds<D>;
@@ -1483,7 +1516,14 @@ __device__ void prefill_pipe_impl(const FaArgs& a) {
   // finalize: O = O / l (0 where no key was visible)
   const float lt = pair_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if (qvalid) {
+  if constexpr (D >= 128) {
+    // O through LDS (store_o_lds) in a private 8 KB slice of the bf16 K tiles, once no DMA,
+    // conversion or read of any wave is in flight
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    float* const ldsw = reinterpret_cast<float*>((wave < 2 ? sKb0 : sKb1) + (wave & 1) * 8192);
+    store_o_lds<D>(o, inv, ldsw, a.o + bh * a.Sq * D, qw0, a.Sq, lane);
+  } else if (qvalid) {
     float* orow = a.o + (bh * a.Sq + qi) * D;
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++)
@@ -1843,34 +1883,11 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const float lt = pair_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   if constexpr (D >= 128 && !TRACE) {
-    // O through LDS, so that every store instruction writes whole 128-byte lines: a lane of
-    // the MFMA layout holds 16-byte pieces of its row 128 bytes apart, whose line-partial
-    // stores cost 20% extra HBM writes.  Per 64-column chunk the wave writes its 32 x 64
-    // floats to a private 8 KB slice of the K tiles (free after the loop's last barrier; the
-    // 16-byte chunk c of row r at c ^ (r & 15)), then reads 4 rows x 256 contiguous bytes per
-    // instruction and stores them non-temporally (O is not read again here: K and V keep
-    // the L2, 96 -> 68 MB fetched on the S = 4096 GQA prefill).
+    // O through LDS (store_o_lds), in a private 8 KB slice of the K tiles, free after the
+    // loop's last barrier (96 -> 68 MB fetched and 161 -> 134 MB written on the S = 4096 GQA
+    // prefill)
     float* const ldsw = reinterpret_cast<float*>(D == 256 ? sKb0 + wave * 8192 : (wave < 2 ? sKb0 : sKb1) + (wave & 1) * 8192);
-#pragma unroll
-    for (int p = 0; p < D / 64; p++) {
-#pragma unroll
-      for (int dd = 0; dd < 2; dd++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int dt = 2 * p + dd, cidx = dd * 8 + 2 * g + h;
-          const float4 w = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                                       o[dt][4 * g + 3] * inv);
-          *reinterpret_cast<float4*>(ldsw + r * 64 + ((cidx ^ (r & 15)) << 2)) = w;
-        }
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const int row = 4 * k + (lane >> 4), c = lane & 15;
-        const float4 v = *reinterpret_cast<const float4*>(ldsw + row * 64 + ((c ^ (row & 15)) << 2));
-        if (qw0 + row < a.Sq)
-          __builtin_nontemporal_store(__builtin_bit_cast(v4i, v),
-                                      reinterpret_cast<v4i*>(a.o + (bh * a.Sq + qw0 + row) * D + 64 * p + 4 * c));
-      }
-    }
+    store_o_lds<D>(o, inv, ldsw, a.o + bh * a.Sq * D, qw0, a.Sq, lane);
   } else if (qvalid) {
     float* orow = a.o + (bh * a.Sq + qi) * D;
 #pragma unroll
