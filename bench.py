@@ -340,7 +340,7 @@ def main():
                     help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode, gemm): W untimed + K timed calls")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this path runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in DESIGN.md)",
+        print("bench.py: this build measures one GPU; --gpus must be 1 (the path is not sharded across GPUs here)",
               file=sys.stderr)
         sys.exit(2)
 
