@@ -1784,7 +1784,9 @@ __device__ void prefill3_impl(const FaArgs& a) {
                            a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
                            a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk, D);
   const P3Lane pl = p3_lane<D, NW>(wave, lane);
-  const float c = SOFTCAP ? 1.0f : (NW == 4 ? in_vgpr(a.c_log2) : a.c_log2);
+  // loop-invariant operands in VGPRs at three waves per SIMD (D <= 128), in SGPRs at two (D =
+  // 256: there an SGPR operand issues at the full-rate op's speed and saves the register)
+  const float c = SOFTCAP ? 1.0f : (D <= 128 ? in_vgpr(a.c_log2) : a.c_log2);
 
   v16f o[D / 32];
 #pragma unroll
@@ -1825,7 +1827,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
       p3_dma_interleave<D>();
     }
     __builtin_amdgcn_s_setprio(0);
-    pipe_scores<SOFTCAP, NW == 4>(sc, a);
+    pipe_scores<SOFTCAP, D <= 128>(sc, a);
     if (need_mask(j)) {
       const int ln = fresh_lane();
       int klo, khi;
