@@ -1814,9 +1814,10 @@ __device__ void prefill3_impl(const FaArgs& a) {
     // nothing reads that stage) are issued between the score MFMAs of block j, or -- one K
     // stage -- once every wave has read K(j), while the MFMAs run
     v16f sc[BN / 32];
-    // the score MFMAs at raised wave priority: the SIMD's arbiter issues them ahead of the
-    // other workgroups' softmax VALU (about 1% faster on the S = 4096 GQA prefill)
-    __builtin_amdgcn_s_setprio(1);
+    // D <= 128: the score MFMAs at raised wave priority, so that the SIMD's arbiter issues them
+    // ahead of the other two workgroups' softmax VALU (about 1% faster on the S = 4096 GQA
+    // prefill); D = 256 (two waves per SIMD) runs about 0.5% faster without it
+    if constexpr (D <= 128) __builtin_amdgcn_s_setprio(1);
     p3_qk<D>(sc, qb, kb_cur, fresh_lane());
     if constexpr (K1) {
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's K operand reads are done
@@ -1826,7 +1827,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
       p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
       p3_dma_interleave<D>();
     }
-    __builtin_amdgcn_s_setprio(0);
+    if constexpr (D <= 128) __builtin_amdgcn_s_setprio(0);
     pipe_scores<SOFTCAP, D <= 128>(sc, a);
     if (need_mask(j)) {
       const int ln = fresh_lane();
