@@ -118,11 +118,11 @@ mxfa_status mxfa_prefill(const mxfa_attn_params *p,
                          const uint8_t *v, const uint8_t *v_sc,
                          float *o, void *stream);
 
-/* Prefill with a caller workspace, the faster path for every shape.  First launches write the
+/* Prefill with a caller workspace, the faster path for every shape.  A first launch writes the
  * bf16 value of every K element (E4M3 code x 2^(scale - 127), exact in bf16) and, for E3M2 V,
  * the E4M3 code of every V element (the same value) into the workspace; the attention kernel
  * then streams those copies into LDS by DMA: three 4-wave workgroups per CU for head_dim <= 128,
- * one 8-wave workgroup (two waves per SIMD) for head_dim 256.  Same inputs, outputs and O as
+ * two (two waves per SIMD) for head_dim 256.  Same inputs, outputs and O as
  * mxfa_prefill within the tolerance of the reference's algorithm (bit-identical to it for
  * head_dim <= 128 with E4M3 V, where both run the same arithmetic in the same order).
  * *workspace_bytes = batch * num_kv_heads * seq_k * head_dim * (2, or 3 with E3M2 V).  A
