@@ -128,19 +128,45 @@ def time_calls(torch, fn, steps, warmup, preheat=True):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_hbm_traffic.txt")
+KERNEL_SOURCE = os.path.join(ROOT, "radiance-kernels_amd", "csrc", "mxfa_kernels.hip")
+
+
+def kernel_source_sha():
+    """sha256 (first 16 hex digits) of the kernel source the code object is built from."""
+    import hashlib
+    with open(KERNEL_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def profile_fields(path, keys):
+    """key: value lines of a committed rocprofv3 summary (None when absent)."""
+    out = dict.fromkeys(keys)
+    try:
+        with open(path) as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                if k in out:
+                    out[k] = v.strip()
+    except OSError:
+        pass
+    return out
 
 
 def measured_traffic():
-    """HBM bytes per prefill launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
-    WRITE_SIZE, each scaled by its plain-copy calibration factor), or None."""
-    try:
-        with open(TRAFFIC_PROFILE) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
-    except OSError:
-        pass
-    return None
+    """HBM bytes per prefill step from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE of both launches of a call, each scaled by its plain-copy calibration factor):
+    {"step": bytes, "attention": bytes, "prepass": bytes, "source": ..., "kernel_source_sha":
+    sha of the profiled source, "current": whether it is the source of this build}, or None."""
+    f = profile_fields(TRAFFIC_PROFILE, ("traffic_bytes_per_step", "traffic_bytes_per_launch",
+                                         "prepass_traffic_bytes", "kernel_source_sha256"))
+    if f["traffic_bytes_per_launch"] is None:
+        return None
+    att = int(f["traffic_bytes_per_launch"])
+    pre = int(f["prepass_traffic_bytes"]) if f["prepass_traffic_bytes"] else None
+    step = int(f["traffic_bytes_per_step"]) if f["traffic_bytes_per_step"] else (att + (pre or 0))
+    return {"step": step, "attention": att, "prepass": pre, "source": "profiles/prefill_c3_hbm_traffic.txt",
+            "kernel_source_sha": f["kernel_source_sha256"],
+            "current": f["kernel_source_sha256"] == kernel_source_sha()}
 
 
 COUNTERS_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_counters.txt")
@@ -148,15 +174,49 @@ COUNTERS_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_counters.txt")
 
 def measured_mfma_busy():
     """MFMA-busy % of the configs[2] attention kernel from the committed rocprofv3 --pmc summary
-    (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES x 1024 SIMDs), or None."""
-    try:
-        with open(COUNTERS_PROFILE) as f:
-            for line in f:
-                if line.startswith("mfma_busy_pct:"):
-                    return float(line.split(":")[1])
-    except OSError:
-        pass
-    return None
+    (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES x 1024 SIMDs) -- not measured in this run --
+    with the sha of the kernel source it was profiled from and whether that is this build's."""
+    f = profile_fields(COUNTERS_PROFILE, ("mfma_busy_pct", "kernel_source_sha256"))
+    if f["mfma_busy_pct"] is None:
+        return None
+    return {"pct": float(f["mfma_busy_pct"]), "source": "committed profile profiles/prefill_c3_counters.txt "
+            "(rocprofv3 --pmc; not measured in this run)", "kernel": "mxfa_prefill3_d128",
+            "kernel_source_sha": f["kernel_source_sha256"], "current": f["kernel_source_sha256"] == kernel_source_sha()}
+
+
+# MFMA clocks per wave-block (32 queries x 64 keys) of the workspace prefill: D/16 x 2 score
+# MFMAs v_mfma_f32_32x32x16_bf16 (32 clocks each) and D/32 PV MFMAs
+# v_mfma_scale_f32_32x32x64_f8f6f4 (64 clocks each); 1,024 SIMDs at the 2.4 GHz clock the
+# 5.0 PFLOP/s MXFP8 peak is quoted at.
+PEAK_CLOCK_HZ = 2.4e9
+SIMDS = 1024
+
+
+def prefill3_wave_blocks(mxfa, p):
+    """Wave-blocks one mxfa_prefill_ws call runs: every wave of a workgroup walks the
+    workgroup's key blocks [j0, j1) (the kernel's loop bounds; masked or not)."""
+    group = p.num_q_heads // p.num_kv_heads
+    hpw = next(h for h in (4, 2, 1) if group % h == 0)
+    qpw = 32 * (4 // hpw)
+    n_qblk = -(-p.seq_q // qpw)
+    nkb = -(-p.seq_k // mxfa.DEFAULT_BLOCK_N)
+    per_head_group = 0
+    for qblk in range(n_qblk):
+        q0 = qblk * qpw
+        qmax = min(q0 + qpw, p.seq_q) - 1
+        j0 = max(0, p.q_pos0 + q0 - p.window + 1) // mxfa.DEFAULT_BLOCK_N if p.window > 0 else 0
+        j1 = min(nkb, max(0, p.q_pos0 + qmax) // mxfa.DEFAULT_BLOCK_N + 1) if p.causal else nkb
+        per_head_group += 4 * max(0, j1 - j0)
+    return per_head_group * p.batch * p.num_kv_heads * (group // hpw)
+
+
+def mfma_ceiling(mxfa, p, flops):
+    """The roofline fraction the kernel could reach with its MFMA pipes 100% busy: algorithmic
+    FLOP over the time its MFMA instructions alone take, at the peak's clock."""
+    D = p.head_dim
+    clocks = prefill3_wave_blocks(mxfa, p) * ((D // 16) * 2 * 32 + (D // 32) * 64)
+    t = clocks / SIMDS / PEAK_CLOCK_HZ
+    return flops / t / (MXFP8_PEAK_TFLOPS * 1e12), clocks
 
 
 def calibrate_copy(torch):
@@ -254,12 +314,34 @@ def cpu_threads():
     return max(1, min(n, CPU_THREAD_CAP)), n
 
 
+ORACLE_NATIVE_FLAGS = ["-O3", "-march=native", "-ffp-contract=off", "-fPIC", "-shared", "-std=c11", "-D_GNU_SOURCE"]
+
+
+def native_oracle():
+    """The CPU oracle compiled on this host with -march=native (the baseline build the plan
+    names), into a temporary directory; (path, flags) or (None, reason) when no compiler runs."""
+    import subprocess
+    import tempfile
+    d = tempfile.mkdtemp(prefix="mxfa_oracle_")
+    out = os.path.join(d, "liboracle_native.so")
+    cmd = [os.environ.get("CC", "gcc")] + ORACLE_NATIVE_FLAGS + ["-o", out, os.path.join(ROOT, "oracle", "mx_oracle.c"),
+                                                                 "-lm", "-lpthread"]
+    try:
+        subprocess.run(cmd, check=True, capture_output=True, timeout=120)
+        return out, " ".join(ORACLE_NATIVE_FLAGS)
+    except (OSError, subprocess.SubprocessError) as e:
+        return None, f"native build failed ({e.__class__.__name__}); the prebuilt -O3 oracle ran instead"
+
+
 def cpu_baseline(mxfa, p, ops_host, threads, visible):
     """The CPU oracle (this repo's C restatement of the reference algorithm, threaded over
     query heads) on the whole configs[2] workload: every (batch, query head), the same
-    block size.  About 40 thread-seconds of CPU work."""
+    block size.  About 40 thread-seconds of CPU work.  Built here with -O3 -march=native."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
+    lib_path, flags = native_oracle()
+    if lib_path:
+        O.LIB_PATH = lib_path
     op = O.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim,
                        causal=bool(p.causal), scale=p.softmax_scale)
     t0 = time.time()
@@ -267,7 +349,7 @@ def cpu_baseline(mxfa, p, ops_host, threads, visible):
     dt = time.time() - t0
     flops = mxfa.attention_flops(p)
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "cpu_model": cpu_model(), "cpus_visible": visible,
+            "cpu_model": cpu_model(), "cpus_visible": visible, "build": flags,
             "sample": f"all of configs[2]: {p.batch} x {p.num_q_heads} query heads ({flops / 1e9:.1f} GFLOP, "
                       f"{dt:.2f} s wall on {threads} threads of {visible} visible; the GPU box gives one GPU "
                       f"{CPU_THREAD_CAP} host threads)"}
@@ -382,10 +464,19 @@ def main():
                    "causal": True, "block_n": mxfa.DEFAULT_BLOCK_N, "gflop_per_step": round(flops / 1e9, 2)},
         "pct_mxfp8_peak": round(100.0 * tflops / MXFP8_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic()},
-        "mfma_busy": {"pct": measured_mfma_busy(), "source": "profiles/prefill_c3_counters.txt",
-                      "kernel": "mxfa_prefill3_d128"},
+                     "frac": round(tflops / MXFP8_PEAK_TFLOPS, 4), "traffic": None},
+        "mfma_busy_from_profile": measured_mfma_busy(),
     }
+    tr = measured_traffic()
+    if tr is not None:
+        result["roofline"]["traffic"] = tr["step"]
+        result["roofline"]["traffic_detail"] = tr
+    ceil, clocks = mfma_ceiling(mxfa, p, flops)
+    result["roofline"]["mfma_ceiling"] = round(ceil, 4)
+    result["roofline"]["mfma_ceiling_basis"] = (
+        f"{clocks / 1e6:.1f} M SIMD-clocks of MFMA per step ({prefill3_wave_blocks(mxfa, p)} wave-blocks x "
+        f"{(p.head_dim // 16) * 64 + (p.head_dim // 32) * 64} clocks: bf16 QK^T + MXFP8 PV) over {SIMDS} SIMDs at "
+        f"{PEAK_CLOCK_HZ / 1e9:.1f} GHz; 0.5 of peak needs the MFMA pipes {50.0 / ceil:.0f}% busy")
 
     # the same workload with the reference device kernels' P rule (R2 compatibility mode)
     p2 = mxfa.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim, causal=True,

@@ -22,7 +22,6 @@ struct FaArgs {
   int hpw;            // prefill: query heads per workgroup
   int qpw;            // prefill: query positions per workgroup
   int n_qblk;         // prefill: query blocks; decode: interleaved partials per query head
-  int split_len;      // unused (0)
   int fuse_combine;   // decode (D <= 128): the chunks of a head merge inside the workgroup
   float c_log2;       // softmax_scale * log2(e)  (no softcap)
   float sc_u;         // softmax_scale / softcap

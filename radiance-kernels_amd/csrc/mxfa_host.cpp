@@ -179,6 +179,11 @@ mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
     if (p->num_q_heads / p->num_kv_heads > 32)
       return fail(MXFA_ERR_UNSUPPORTED, "decode supports at most 32 query heads per KV head");
   }
+  // Per (batch, KV head) the kernels address K/V (and the workspace's bf16 K, 2 bytes per
+  // element) through buffer resources of seq_k * 2 * head_dim bytes with 32-bit signed byte
+  // offsets: keep that range below 2^31.
+  if ((int64_t)p->seq_k * 2 * p->head_dim > (int64_t)INT32_MAX)
+    return fail(MXFA_ERR_UNSUPPORTED, "seq_k * head_dim exceeds the kernels' 32-bit K/V range (2^30 elements per head)");
   int64_t qelems = (int64_t)p->batch * p->num_q_heads * p->seq_q * p->head_dim;
   int64_t kelems = (int64_t)p->batch * p->num_kv_heads * (p->kv_stride ? p->kv_stride : p->seq_k) * p->head_dim;
   if (qelems > (int64_t)1 << 40 || kelems > (int64_t)1 << 40) return fail(MXFA_ERR_INVALID_ARG, "tensor too large");

@@ -1818,7 +1818,10 @@ __device__ void prefill3_impl(const FaArgs& a) {
     // ahead of the other two workgroups' softmax VALU (about 1% faster on the S = 4096 GQA
     // prefill); D = 256 (two waves per SIMD) runs about 0.5% faster without it
     if constexpr (D <= 128) __builtin_amdgcn_s_setprio(1);
-    p3_qk<D>(sc, qb, kb_cur, fresh_lane());
+    // the score-operand address from the lane id held across the loop (one register; about
+    // 1% faster on the S = 4096 GQA prefill than recomputing it per block); the softcap
+    // kernels, one register short, recompute it
+    p3_qk<D>(sc, qb, kb_cur, SOFTCAP ? fresh_lane() : lane);
     if constexpr (K1) {
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's K operand reads are done
       __builtin_amdgcn_s_barrier();

@@ -251,7 +251,9 @@ def fill_normal(x, seed, outlier_p=0.0, outlier_mul=20.0, stream=None):
 
 
 def prefill_plan(p):
-    """Workspace bytes of mxfa_prefill_ws for p (0: the shape runs the workspace-free kernel)."""
+    """Workspace bytes of mxfa_prefill_ws for p: the bf16 copy of K (B * Hkv * Sk * D * 2
+    bytes), plus the E4M3 copy of V (B * Hkv * Sk * D bytes) when V is E3M2.  Never 0: every
+    shape runs the workspace kernel."""
     ws = ctypes.c_size_t(0)
     _check(lib().mxfa_prefill_plan(ctypes.byref(p), ctypes.byref(ws)))
     return ws.value

@@ -185,3 +185,22 @@ def test_prefill_plan_and_workspace_checks():
     assert L.mxfa_prefill_ws(ctypes.byref(small), *([ptr] * 7), ptr, need - 1, None) == 5
     assert b"workspace needs" in L.mxfa_last_error()
     assert L.mxfa_prefill_ws(ctypes.byref(small), *([None] * 7), ptr, need, None) == 1
+
+
+def test_kv_range_limit_rejected_without_device():
+    """The kernels address one (batch, KV head) of K/V -- and the workspace's bf16 K, two
+    bytes per element -- with 32-bit byte offsets: seq_k * head_dim * 2 must stay below 2^31.
+    Shapes past it are MXFA_ERR_UNSUPPORTED at plan time (no device needed); the largest
+    shape inside it is accepted."""
+    L = mxfa.lib()
+    ws = ctypes.c_size_t(0)
+    for d in (64, 128, 256):
+        limit = (2 ** 31 - 1) // (2 * d) // 32 * 32          # largest seq_k (multiple of 32) inside
+        ok = mxfa.make_params(1, 1, 1, 1, limit, d)
+        assert L.mxfa_prefill_plan(ctypes.byref(ok), ctypes.byref(ws)) == 0
+        assert ws.value == limit * d * 2
+        bad = mxfa.make_params(1, 1, 1, 1, limit + 32, d)
+        assert L.mxfa_prefill_plan(ctypes.byref(bad), ctypes.byref(ws)) == 2
+        assert b"32-bit K/V range" in L.mxfa_last_error()
+        dec = mxfa.make_params(1, 1, 1, 1, limit + 32, d, causal=True, q_pos0=limit + 31)
+        assert L.mxfa_decode_plan(ctypes.byref(dec), ctypes.byref(ctypes.c_int32()), ctypes.byref(ws)) == 2

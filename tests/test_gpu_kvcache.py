@@ -121,3 +121,38 @@ def test_decode_in_place_on_cache_with_capacity():
     rel, mab = errors(np_(got), want)
     print(f"   in-place decode: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
     assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+
+
+@pytest.mark.parametrize("D,fmt", [(64, mxfa.FMT_E3M2), (128, mxfa.FMT_E4M3), (256, mxfa.FMT_E3M2),
+                                   (256, mxfa.FMT_E4M3)])
+def test_prefill_in_place_on_strided_cache(D, fmt):
+    """Prefill with several query tiles (Sq > 32) over caches whose rows are kv_stride >
+    seq_k apart, the rows past seq_k holding garbage codes: the workspace prefill (its
+    pre-pass reads K -- and E3M2 V -- at the cache stride) and the workspace-free kernel
+    (pipe kernel for D <= 128 with E4M3 V, staged kernel otherwise) give O bit for bit equal
+    to the same calls on dense copies of the first seq_k keys, within tolerance of the oracle."""
+    B, Hq, Hkv, Sq, Sk, Lcap = 2, 4, 2, 96, 160, 256
+    rng = np.random.default_rng(430 + D + 7 * fmt)
+    Q = torch.from_numpy(rng.standard_normal((B, Hq, Sq, D)).astype(np.float32)).to(DEV)
+    K = torch.from_numpy(rng.standard_normal((B, Hkv, Sk, D)).astype(np.float32)).to(DEV)
+    V = torch.from_numpy(rng.standard_normal((B, Hkv, Sk, D)).astype(np.float32)).to(DEV)
+    q, qs = mxfa.quantize_rows(Q)
+    k, ks = mxfa.quantize_rows(K)
+    v, vs = mxfa.quantize_cols(V, fmt)
+    garbage = lambda shape: torch.from_numpy(rng.integers(0, 256, shape, dtype=np.uint8)).to(DEV)  # noqa: E731
+    kc, ksc = garbage((B, Hkv, Lcap, D)), garbage((B, Hkv, Lcap, D // 32))
+    vc, vsc = garbage((B, Hkv, Lcap, D)), garbage((B, Hkv, Lcap // 32, D))
+    kc[:, :, :Sk], ksc[:, :, :Sk], vc[:, :, :Sk], vsc[:, :, :Sk // 32] = k, ks, v, vs
+    kw = dict(causal=True, q_pos0=Sk - Sq, v_fmt=fmt)
+    pd = mxfa.make_params(B, Hq, Hkv, Sq, Sk, D, **kw)
+    ps = mxfa.make_params(B, Hq, Hkv, Sq, Sk, D, kv_stride=Lcap, **kw)
+    for ws in (None, False):
+        dense = mxfa.prefill(pd, q, qs, k, ks, v, vs, workspace=ws)
+        strided = mxfa.prefill(ps, q, qs, kc, ksc, vc, vsc, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(strided, dense), ("workspace" if ws is None else "workspace-free", D, fmt)
+    want = O.attention(oracle_params(pd), np_(q), np_(qs), np_(k), np_(ks), np_(v), np_(vs),
+                       block_n=mxfa.DEFAULT_BLOCK_N)
+    rel, mab = errors(np_(strided), want)
+    print(f"   strided-cache prefill D={D} fmt={fmt}: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
