@@ -39,13 +39,11 @@ mxfa_status fail(mxfa_status st, const std::string& msg) {
 
 const char* const kKernelNames[] = {
     "mxfa_quant_rows_e4m3",    "mxfa_quant_rows_e3m2",    "mxfa_quant_cols_e4m3", "mxfa_quant_cols_e3m2",
-    "mxfa_softmax_requant_rows",     "mxfa_fill_normal_f32",    "mxfa_prefill_d64",     "mxfa_prefill_d128",
-    "mxfa_prefill_d256",       "mxfa_prefill_d64_softcap", "mxfa_prefill_d128_softcap", "mxfa_prefill_d256_softcap",
+    "mxfa_softmax_requant_rows",     "mxfa_fill_normal_f32",
     "mxfa_decode_d64",         "mxfa_decode_d128",        "mxfa_decode_d256",     "mxfa_decode_d64_softcap",
     "mxfa_decode_d128_softcap", "mxfa_decode_d256_softcap", "mxfa_decode_combine", "mxfa_kv_append_e4m3",
     "mxfa_kv_append_e3m2",     "mxfa_kv_tail_update",     "mxfa_quant_rows_r4",
-    "mxfa_prefill_d64_r2",     "mxfa_prefill_d128_r2",    "mxfa_prefill_d256_r2",  "mxfa_prefill_d64_softcap_r2",
-    "mxfa_prefill_d128_softcap_r2", "mxfa_prefill_d256_softcap_r2", "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
+    "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
     "mxfa_decode_d256_r2",     "mxfa_decode_d64_softcap_r2", "mxfa_decode_d128_softcap_r2",
     "mxfa_decode_d256_softcap_r2", "mxfa_gemm", "mxfa_gemm_ae3m2", "mxfa_gemm_be3m2", "mxfa_gemm_ae3m2_be3m2",
     "mxfa_prefill_pipe_d64",   "mxfa_prefill_pipe_d128",  "mxfa_prefill_pipe_d64_softcap", "mxfa_prefill_pipe_d128_softcap",
@@ -60,6 +58,11 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3_trace_d64_r2", "mxfa_prefill3_trace_d128_r2", "mxfa_prefill3_trace_d256_r2",
     "mxfa_prefill3_trace_d64_softcap_r2", "mxfa_prefill3_trace_d128_softcap_r2", "mxfa_prefill3_trace_d256_softcap_r2",
     "mxfa_gemm_dma",
+    "mxfa_prefill3n_d256", "mxfa_prefill3n_d256_softcap", "mxfa_prefill3n_d256_r2", "mxfa_prefill3n_d256_softcap_r2",
+    "mxfa_prefill3n_d64_e3m2", "mxfa_prefill3n_d128_e3m2", "mxfa_prefill3n_d256_e3m2",
+    "mxfa_prefill3n_d64_softcap_e3m2", "mxfa_prefill3n_d128_softcap_e3m2", "mxfa_prefill3n_d256_softcap_e3m2",
+    "mxfa_prefill3n_d64_r2_e3m2", "mxfa_prefill3n_d128_r2_e3m2", "mxfa_prefill3n_d256_r2_e3m2",
+    "mxfa_prefill3n_d64_softcap_r2_e3m2", "mxfa_prefill3n_d128_softcap_r2_e3m2", "mxfa_prefill3n_d256_softcap_r2_e3m2",
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -216,10 +219,10 @@ FaArgs make_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* qs,
   return a;
 }
 
-const char* kernel_name(const char* kind, const mxfa_attn_params* p) {
+const char* kernel_name(const char* kind, const mxfa_attn_params* p, bool e3m2_suffix = false) {
   static thread_local char buf[64];
-  std::snprintf(buf, sizeof buf, "mxfa_%s_d%d%s%s", kind, p->head_dim, p->softcap > 0.0f ? "_softcap" : "",
-                p->p_rule == MXFA_P_R2 ? "_r2" : "");
+  std::snprintf(buf, sizeof buf, "mxfa_%s_d%d%s%s%s", kind, p->head_dim, p->softcap > 0.0f ? "_softcap" : "",
+                p->p_rule == MXFA_P_R2 ? "_r2" : "", e3m2_suffix ? "_e3m2" : "");
   return buf;
 }
 
@@ -476,13 +479,6 @@ size_t prefill3_workspace(const mxfa_attn_params* p) {
   return prefill3_kbf_bytes(p) + v;
 }
 
-// MXFA_PREFILL=staged or =pipe selects that kernel for every call (both workspace-free);
-// the switch exists to compare the kernels, which give O within the oracle's tolerance.
-const char* prefill_override() {
-  const char* sel = getenv("MXFA_PREFILL");
-  if (sel && (std::strcmp(sel, "staged") == 0 || std::strcmp(sel, "pipe") == 0)) return sel;
-  return nullptr;
-}
 }  // namespace
 
 extern "C" {
@@ -498,10 +494,11 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, 4, grid);
   void* args[] = {&a};
   // D <= 128 with E4M3 V: the software-pipelined kernel (LDS-DMA staging, score MFMAs of
-  // the next block inside the softmax); D = 256 and E3M2 V: the staged kernel.
-  const char* sel = prefill_override();
-  const bool staged = (sel && std::strcmp(sel, "staged") == 0) || p->head_dim > 128 || p->v_fmt != MXFA_FMT_E4M3;
-  return launch(dm, kernel_name(staged ? "prefill" : "prefill_pipe", p), grid, dim3(256), args, stream);
+  // the next block inside the softmax); D = 256 and E3M2 V: the workspace kernel's design in
+  // its workspace-free form (K widened to bf16 in LDS, E3M2 V read as E5M2).
+  if (p->head_dim <= 128 && p->v_fmt == MXFA_FMT_E4M3)
+    return launch(dm, kernel_name("prefill_pipe", p), grid, dim3(256), args, stream);
+  return launch(dm, kernel_name("prefill3n", p, p->v_fmt == MXFA_FMT_E3M2), grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_prefill_plan(const mxfa_attn_params* p, size_t* workspace_bytes) {
@@ -572,7 +569,6 @@ mxfa_status mxfa_prefill_ws(const mxfa_attn_params* p, const uint8_t* q, const u
                             const uint8_t* k_sc, const uint8_t* v, const uint8_t* v_sc, float* o, void* workspace,
                             size_t workspace_bytes, void* stream) {
   if (mxfa_status st = check_params(p, false)) return st;
-  if (prefill_override()) return mxfa_prefill(p, q, q_sc, k, k_sc, v, v_sc, o, stream);
   return prefill_ws_impl(p, q, q_sc, k, k_sc, v, v_sc, o, workspace, workspace_bytes, stream, nullptr);
 }
 

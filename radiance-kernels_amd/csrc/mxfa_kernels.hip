@@ -347,6 +347,10 @@ __device__ __forceinline__ float pair_sum(float x) {
 __device__ __forceinline__ v16f mfma_mx(v8i a, v8i b, v16f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
 }
+// A operand in E5M2 (cbsz = 1), B in E4M3
+__device__ __forceinline__ v16f mfma_mx_a5(v8i a, v8i b, v16f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 0, 0, sa, 0, sb);
+}
 
 __device__ __forceinline__ v16f mfma_bf16(v4i a, v4i b, v16f c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
@@ -369,19 +373,6 @@ __device__ __forceinline__ v8i cat44(v4i lo, v4i hi) {
   return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Per-tile staging of one key block: K and V codes (BN x D) and their scales.
-template <int D>
-struct BlockRegs {
-  static constexpr int CPR = D / 16;                 // 16-byte chunks per row
-  static constexpr int NCH = BN * CPR;               // chunks per matrix
-  static constexpr int PER = NCH / (NWAVE * 64);     // chunks per thread (2, 4 or 8 with 256 threads... )
-  static constexpr int SCH = BN * D / 32 / 16;       // 16-byte scale chunks per matrix
-  v4i k[PER > 0 ? PER : 1];
-  uint32_t kscale[PER > 0 ? PER : 1];   // E8M0 scale of each K chunk's 32-block
-  v4i v[PER > 0 ? PER : 1];
-  v4i vsc;
-};
-
 // LDS tiles: K as bf16 (row pitch 2D + 16 bytes), V as fp8 codes (pitch D + 16);
 // the 16-byte pads keep row starts on distinct banks.
 template <int D> struct Lds {
@@ -396,31 +387,6 @@ template <int D> struct Lds {
 // key rows >= Sk need no branch.  Word 3 = raw 32-bit data format (gfx9 buffer layout).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const uint8_t* base, int64_t off, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), 0, (int)(bytes > 0 ? bytes : 0), 0x00020000);
-}
-
-// Global -> registers for key block starting at key0 (rows >= Sk read as 0).
-template <int D>
-__device__ __forceinline__ void load_block(BlockRegs<D>& r, const uint8_t* __restrict__ kb, const uint8_t* __restrict__ ksb,
-                                           const uint8_t* __restrict__ vb, const uint8_t* __restrict__ vsb,
-                                           int key0, int Sk, int tid) {
-  constexpr int CPR = BlockRegs<D>::CPR;
-  const int nk = Sk - key0;
-  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kb, (int64_t)key0 * D, (int64_t)nk * D);
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vb, (int64_t)key0 * D, (int64_t)nk * D);
-  const __amdgpu_buffer_rsrc_t rks = buf_rsrc(ksb, (int64_t)key0 * (D / 32), (int64_t)nk * (D / 32));
-#pragma unroll
-  for (int i = 0; i < BlockRegs<D>::PER; i++) {
-    const int c = tid + i * NWAVE * 64;
-    const int row = c / CPR, col = (c % CPR) * 16;
-    r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, row * D + col, 0, 0);
-    r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, row * D + col, 0, 0);
-    r.kscale[i] = __builtin_amdgcn_raw_buffer_load_b8(rks, row * (D / 32) + col / 32, 0, 0);
-  }
-  constexpr int SCH = BlockRegs<D>::SCH;
-  if (tid < SCH) {                                     // V scales: [key/32][D]
-    const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(vsb, (int64_t)(key0 / 32) * D, (int64_t)(Sk / 32 - key0 / 32) * D);
-    r.vsc = __builtin_amdgcn_raw_buffer_load_b128(rvs, tid * 16, 0, 0);
-  }
 }
 
 // The same loads through buffer resources over one (b, KV head)'s K, K scales, V and V
@@ -440,48 +406,6 @@ __device__ __forceinline__ KvRsrc kv_rsrc(const uint8_t* kb, const uint8_t* ksb,
   r.v = buf_rsrc(vb, 0, (int64_t)Sk * D);
   r.vs = buf_rsrc(vsb, 0, (int64_t)(Sk / 32) * D);
   return r;
-}
-
-template <int D>
-__device__ __forceinline__ void load_block(BlockRegs<D>& r, const KvRsrc& rs, int key0, int tid) {
-  constexpr int CPR = BlockRegs<D>::CPR;
-#pragma unroll
-  for (int i = 0; i < BlockRegs<D>::PER; i++) {
-    const int c = tid + i * NWAVE * 64;
-    const int row = c / CPR, col = (c % CPR) * 16;
-    r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.k, (key0 + row) * D + col, 0, 0);
-    r.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs.v, (key0 + row) * D + col, 0, 0);
-    r.kscale[i] = __builtin_amdgcn_raw_buffer_load_b8(rs.ks, (key0 + row) * (D / 32) + col / 32, 0, 0);
-  }
-  constexpr int SCH = BlockRegs<D>::SCH;
-  if (tid < SCH) r.vsc = __builtin_amdgcn_raw_buffer_load_b128(rs.vs, (key0 / 32) * D + tid * 16, 0, 0);  // [key/32][D]
-}
-
-// Registers -> LDS: K dequantized to bf16, V codes (E3M2 widened to E4M3), V scales.
-template <int D>
-__device__ __forceinline__ void store_block(const BlockRegs<D>& r, uint8_t* sKb, uint8_t* sV, uint8_t* sVs, int tid,
-                                            int v_e3m2) {
-  constexpr int CPR = BlockRegs<D>::CPR;
-  constexpr int KP = Lds<D>::KP;
-  constexpr int KPB = Lds<D>::KPB;
-#pragma unroll
-  for (int i = 0; i < BlockRegs<D>::PER; i++) {
-    int c = tid + i * NWAVE * 64;
-    int row = c / CPR, col = (c % CPR) * 16;
-    float sc = e8m0_as_float(r.kscale[i]);
-    v4i b0 = fp8x8_to_bf16x8((uint32_t)r.k[i][0], (uint32_t)r.k[i][1], sc);
-    v4i b1 = fp8x8_to_bf16x8((uint32_t)r.k[i][2], (uint32_t)r.k[i][3], sc);
-    *reinterpret_cast<v4i*>(sKb + row * KPB + col * 2) = b0;
-    *reinterpret_cast<v4i*>(sKb + row * KPB + col * 2 + 16) = b1;
-    v4i vv = r.v[i];
-    if (v_e3m2) {
-#pragma unroll
-      for (int w = 0; w < 4; w++) vv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)vv[w]);
-    }
-    *reinterpret_cast<v4i*>(sV + row * KP + col) = vv;
-  }
-  constexpr int SCH = BlockRegs<D>::SCH;
-  if (tid < SCH) *reinterpret_cast<v4i*>(sVs + tid * 16) = r.vsc;
 }
 
 // Per-wave online-softmax state and O accumulator for 32 query columns.
@@ -784,154 +708,6 @@ __device__ __forceinline__ void load_q_split(v4i* qb, const uint8_t* qrow, const
   }
 }
 
-// ---------------------------------------------------------------------------
-// Prefill.  Workgroup = 4 waves; wave w handles 32 query positions of one head.
-// The workgroup covers hpw heads of one KV group x qpw positions, so the K/V
-// tile in LDS serves 4 x 32 query rows.  grid = (n_qblk, B * Hkv * group / hpw).
-// ---------------------------------------------------------------------------
-template <int D, bool SOFTCAP, int PR>
-__device__ void prefill_impl(const FaArgs& a) {
-  __shared__ __attribute__((aligned(16))) uint8_t sK[2][Lds<D>::TILEK];
-  __shared__ __attribute__((aligned(16))) uint8_t sV[2][Lds<D>::TILE];
-  __shared__ __attribute__((aligned(16))) uint8_t sVs[2][Lds<D>::SC];
-
-  // wave index through readfirstlane: everything derived from it stays in SGPRs and the
-  // per-block branches below are uniform
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 31, h = lane >> 5;
-  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
-  // renumber them so that each XCD receives a contiguous range of work items, i.e.
-  // all query blocks of the same KV head land on one XCD and share its L2.
-  // When an XCD's range holds whole heads, its heads are interleaved in dispatch order
-  // (every head's first query-block item, then every head's second, ...), so under
-  // causal masking all its heads' longest blocks start first.
-  const int nwg = (int)(gridDim.x * gridDim.y);
-  const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
-  const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
-  const int start_x = xcd * per + min(xcd, rem), cnt_x = per + (xcd < rem ? 1 : 0);
-  const int li = lin >> 3;
-  const int nh_x = cnt_x / a.n_qblk;
-  const bool whole_heads = start_x % a.n_qblk == 0 && cnt_x % a.n_qblk == 0;
-  const int item = start_x + (whole_heads ? (li % nh_x) * a.n_qblk + li / nh_x : li);
-  const int qx = item % a.n_qblk, qy = item / a.n_qblk;
-  const int qblk = a.causal ? (a.n_qblk - 1 - qx) : qx;   // longest rows first
-  const int chunks = a.group / a.hpw;
-  const int bk = qy / chunks;                        // b * Hkv + kvh
-  const int hc = qy % chunks;
-  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
-  const int head = kvh * a.group + hc * a.hpw + (wave % a.hpw);
-  const int q0 = qblk * a.qpw;                      // first query row of the workgroup
-  const int qw0 = q0 + (wave / a.hpw) * 32;         // first query row of this wave
-  const int qi = qw0 + r;
-  const bool qvalid = qi < a.Sq;
-  const int qpos = a.q_pos0 + qi;
-
-  const int64_t bh = (int64_t)b * a.Hq + head;
-  v4i qb[D / 16];
-  load_q<D>(qb, a.q + (bh * a.Sq + qi) * D, a.qs + (bh * a.Sq + qi) * (D / 32), qvalid, h);
-  int klo, khi;
-  key_limits(a, qpos, qvalid, klo, khi);
-
-  // key-block range of the workgroup
-  const int qmax_wg = min(q0 + a.qpw, a.Sq) - 1;
-  const int nkb = (a.Sk + BN - 1) / BN;
-  int j0 = 0, j1 = nkb;
-  if (a.window > 0) j0 = max(0, a.q_pos0 + q0 - a.window + 1) / BN;
-  if (a.causal) j1 = min(nkb, max(0, a.q_pos0 + qmax_wg) / BN + 1);
-  // wave's query-position range (for skipping and mask decisions)
-  const int wq_lo = a.q_pos0 + qw0, wq_hi = a.q_pos0 + min(qw0 + 31, a.Sq - 1);
-  const bool wave_live = qw0 < a.Sq;
-
-  const uint8_t* kb = a.k + (int64_t)bk * a.Skc * D;
-  const uint8_t* ksb = a.ks + (int64_t)bk * a.Skc * (D / 32);
-  const uint8_t* vb = a.v + (int64_t)bk * a.Skc * D;
-  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Skc / 32) * D;
-
-  WaveState<D> st;
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) st.o[dt] = (v16f){};
-  st.m = -INFINITY;
-  st.l = 0.0f;
-
-  auto compute = [&](int j, int buf) {
-    const int key0 = j * BN, key1 = key0 + BN - 1;
-    bool skip = !wave_live || (a.causal && key0 > wq_hi) || (a.window > 0 && key1 + a.window <= wq_lo);
-    if (!skip) {
-      const bool need_mask = __builtin_amdgcn_readfirstlane(
-          (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
-          (qw0 + 31 >= a.Sq));
-      wave_block<D, SOFTCAP, PR>(st, qb, sK[buf], sV[buf], sVs[buf], key0, klo, khi, need_mask, a, lane);
-    }
-  };
-  if constexpr (D <= 128) {
-    const KvRsrc rs = kv_rsrc<D>(kb, ksb, vb, vsb, a.Sk);
-    // Two register stages: block j+1 is loaded during iteration j-1 and stored to LDS at
-    // the end of iteration j, so each global load has a whole iteration to land.
-    BlockRegs<D> ra, rb;
-    if (j0 < j1) load_block<D>(ra, rs, j0 * BN, tid);
-    if (j0 + 1 < j1) load_block<D>(rb, rs, (j0 + 1) * BN, tid);
-    if (j0 < j1) store_block<D>(ra, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
-    __syncthreads();
-    auto step = [&](int j, BlockRegs<D>& nxt2, const BlockRegs<D>& nxt1) {
-      const int buf = (j - j0) & 1;
-      if (j + 2 < j1) load_block<D>(nxt2, rs, (j + 2) * BN, tid);
-      compute(j, buf);
-      if (j + 1 < j1) store_block<D>(nxt1, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
-      __syncthreads();
-    };
-    for (int j = j0; j < j1; j += 2) {
-      step(j, ra, rb);                // ra was stored last step: refill it with j+2; rb holds j+1
-      if (j + 1 < j1) step(j + 1, rb, ra);
-    }
-  } else {
-    // One register stage (register budget of D = 256): block j+1 loads during block j.
-    BlockRegs<D> regs;
-    if (j0 < j1) {
-      load_block<D>(regs, kb, ksb, vb, vsb, j0 * BN, a.Sk, tid);
-      store_block<D>(regs, sK[0], sV[0], sVs[0], tid, a.v_e3m2);
-    }
-    __syncthreads();
-    for (int j = j0; j < j1; j++) {
-      const int buf = (j - j0) & 1;
-      if (j + 1 < j1) load_block<D>(regs, kb, ksb, vb, vsb, (j + 1) * BN, a.Sk, tid);
-      compute(j, buf);
-      if (j + 1 < j1) store_block<D>(regs, sK[buf ^ 1], sV[buf ^ 1], sVs[buf ^ 1], tid, a.v_e3m2);
-      __syncthreads();
-    }
-  }
-
-  // ---- finalize: O = O / l (0 where no key was visible)
-  float l = pair_sum(st.l);
-  float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  if (qvalid) {
-    float* orow = a.o + (bh * a.Sq + qi) * D;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        float4 w = make_float4(st.o[dt][4 * g] * inv, st.o[dt][4 * g + 1] * inv, st.o[dt][4 * g + 2] * inv,
-                               st.o[dt][4 * g + 3] * inv);
-        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * h) = w;
-      }
-  }
-}
-
-// Two workgroups per CU at D <= 128; D = 256 (about 470 registers per lane) fits one.
-template <int D> struct PrefillOcc { static constexpr int N = D == 256 ? 1 : 2; };
-#define MXFA_PREFILL(D, SC, PR, NAME)                                                                  \
-  extern "C" __global__ void __launch_bounds__(256, PrefillOcc<D>::N) NAME(FaArgs a) { prefill_impl<D, SC, PR>(a); }
-MXFA_PREFILL(64, false, P_R1, mxfa_prefill_d64)
-MXFA_PREFILL(128, false, P_R1, mxfa_prefill_d128)
-MXFA_PREFILL(256, false, P_R1, mxfa_prefill_d256)
-MXFA_PREFILL(64, true, P_R1, mxfa_prefill_d64_softcap)
-MXFA_PREFILL(128, true, P_R1, mxfa_prefill_d128_softcap)
-MXFA_PREFILL(256, true, P_R1, mxfa_prefill_d256_softcap)
-MXFA_PREFILL(64, false, P_R2, mxfa_prefill_d64_r2)
-MXFA_PREFILL(128, false, P_R2, mxfa_prefill_d128_r2)
-MXFA_PREFILL(256, false, P_R2, mxfa_prefill_d256_r2)
-MXFA_PREFILL(64, true, P_R2, mxfa_prefill_d64_softcap_r2)
-MXFA_PREFILL(128, true, P_R2, mxfa_prefill_d128_softcap_r2)
-MXFA_PREFILL(256, true, P_R2, mxfa_prefill_d256_softcap_r2)
 
 // ---------------------------------------------------------------------------
 // Prefill, D <= 128, E4M3 V: software-pipelined.  Iteration j runs the softmax and P
@@ -1155,12 +931,14 @@ __device__ __forceinline__ float pair_min_raw(float x) {
 // without a softcap.  The score is non-increasing in r (fma rounds monotonically), so the
 // tile maximum is cap + cap2 * min(r), bit for bit the maximum of the capped scores, and
 // -inf for a fully masked tile (cap2 * inf).
-template <bool SOFTCAP, int PR>
+// VG: the softcap constants in VGPRs (full-rate VALU at three waves per SIMD); at two waves
+// per SIMD SGPR operands cost nothing and save the registers.
+template <bool SOFTCAP, int PR, bool VG = true>
 __device__ __forceinline__ void pipe_softmax(float& m, float& l, v16f (&s)[BN / 32],
                                              v8i& pb, int (&psc)[BN / 32], float& corr, float c,
                                              float cap2 = 0.0f, float cap = 0.0f) {
   constexpr int NT = BN / 32;
-  if (SOFTCAP) {
+  if (SOFTCAP && VG) {
     cap2 = in_vgpr(cap2);
     cap = in_vgpr(cap);
   }
@@ -1294,7 +1072,7 @@ __device__ __forceinline__ void pipe_pv(v16f (&o)[D / 32], const PvRegs<D>& pr, 
 
 // PV of one block in NP parts of D / NP columns: the operand registers of one part at a time
 // (D = 256 at two waves per SIMD: 32 registers instead of 64).
-template <int D, int NP>
+template <int D, int NP, bool V5 = false>
 __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, const v8i& pb, const int (&psc)[BN / 32],
                                          int lane) {
   constexpr int NT = D / 32 / NP;
@@ -1329,7 +1107,9 @@ __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, c
       vs[u] = sv[PipeLds<D>::V + h * D + dt * 32 + r];
     }
 #pragma unroll
-    for (int u = 0; u < NT; u++) o[part * NT + u] = mfma_mx(va[u], pb, o[part * NT + u], vs[u], pscale);
+    for (int u = 0; u < NT; u++)
+      o[part * NT + u] = V5 ? mfma_mx_a5(va[u], pb, o[part * NT + u], vs[u], pscale)
+                            : mfma_mx(va[u], pb, o[part * NT + u], vs[u], pscale);
     if (part + 1 < NP) __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -1380,7 +1160,7 @@ __device__ void prefill_pipe_impl(const FaArgs& a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   // workgroup -> work item: contiguous ranges per XCD, heads interleaved, longest first
-  // (as prefill_impl)
+  // (the same map as prefill3_impl)
   const int nwg = (int)(gridDim.x * gridDim.y);
   const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
   const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
@@ -1724,6 +1504,82 @@ __device__ __forceinline__ void p3_qk(v16f (&s)[BN / 32], const v4i* qb, const u
       s[t] = mfma_bf16(*reinterpret_cast<const v4i*>(kbase + t * 2 * (32 * D) + kk * 512), qb[kk], s[t]);
 }
 
+// ---- Workspace-free form (mxfa_prefill): K arrives as E4M3 codes and is widened in LDS.
+// The fp8 codes of the 16 key rows of group g land in the upper half of that group's bf16
+// region of the chunk-major tile (g * 32D + 16D .. + 16D), 16-byte chunk (row r, column
+// chunk cc) at chunk position 16 cc + r, so that the conversion's reads are contiguous per
+// lane; wave g widens group g in place (every code read before its first bf16 store; one
+// wave's LDS operations complete in order), so no other wave touches that region.  The K
+// scales [BN][D / 32] go to their own small array.
+struct P3NSrc {
+  __amdgpu_buffer_rsrc_t k8, ks, v, vs;
+};
+
+template <int D>
+__device__ __forceinline__ void p3n_dma(const P3NSrc& src, uint8_t* kb, uint8_t* ksc, uint8_t* v, int key0, int wave,
+                                        int lane, const P3Lane& pl) {
+  using L = P3Lds<D>;
+  constexpr int KI = 16 * D / 1024;                     // 1 KB instructions per 16-row fp8 group
+  const int g = wave;
+  const int vk = (lane % 16) * D + (lane / 16) * 16;
+#pragma unroll
+  for (int m = 0; m < KI; m++)
+    dma_lds<16>(src.k8, kb + g * (32 * D) + 16 * D + m * 1024, vk, (key0 + 16 * g) * D + 64 * m);
+  // K scales: BN * D / 32 bytes, 256 per dword instruction, from waves 0 (and 1 at D = 256)
+  if (wave < (BN * D / 32 + 255) / 256) dma_lds<4>(src.ks, ksc + wave * 256, lane * 4, key0 * (D / 32) + wave * 256);
+  // V codes and scales as the workspace form
+  constexpr int VPW = L::VDMA / 4;
+  const int i0 = p3_v_instr<D, 4>(wave, 0);
+#pragma unroll
+  for (int m = 0; m < VPW; m++) {
+    const int i = p3_v_instr<D, 4>(wave, m);
+    dma_lds<16>(src.v, v + i * 1024, pl.v, key0 * D + (i - i0) * 1024);
+  }
+#pragma unroll
+  for (int m = 0; m < (2 * D + 255) / 256; m++) dma_lds<4>(src.vs, v + L::V + m * 256, pl.s, (key0 / 32) * D + m * 256);
+}
+
+// Wave g widens its 16-row group: D / 64 chunks of 16 codes per lane (chunk position lane +
+// 64 i: row lane % 16, column chunk cc = lane / 16 + 4 i), exact bf16 (code x 2^(scale -
+// 127)), stored as the two bf16 chunks 2 cc and 2 cc + 1 of the row (16 lanes: 256
+// contiguous bytes).  Chunk i is read, then stored: its stores cover group bytes [2048 i,
+// 2048 i + 2048), below every later read (16 D + 1024 j for j > i, since i < D / 64), so
+// one chunk at a time is in registers.
+template <int D>
+__device__ __forceinline__ void p3n_widen_k(uint8_t* kb, const uint8_t* ksc, int wave, int lane) {
+  constexpr int NI = D / 64;
+  uint8_t* grp = kb + wave * (32 * D);
+  const int rr = lane % 16;
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int cc = lane / 16 + 4 * i;
+    const v4i x = *reinterpret_cast<const v4i*>(grp + 16 * D + 16 * (lane + 64 * i));
+    const float f = e8m0_as_float(ksc[(16 * wave + rr) * (D / 32) + cc / 2]);
+    *reinterpret_cast<v4i*>(grp + 256 * (2 * cc) + 16 * rr) = fp8x8_to_bf16x8((uint32_t)x[0], (uint32_t)x[1], f);
+    *reinterpret_cast<v4i*>(grp + 256 * (2 * cc + 1) + 16 * rr) = fp8x8_to_bf16x8((uint32_t)x[2], (uint32_t)x[3], f);
+  }
+}
+
+// E3M2 V codes (low 6 bits) -> E5M2 codes of the same bits moved (sign 5 -> 7): an E5M2 byte
+// with exponent field e3 and mantissa m2 is the E3M2 value x 2^-12, subnormals included
+// (2^-14 x 0.m vs 2^-2 x 0.m), so the PV MFMA reads V as E5M2 and O is scaled by 2^12 at the
+// end (exact).  The tile's BN x D bytes, 16 per thread and pass, rewritten in place.
+template <int D>
+__device__ __forceinline__ void p3n_v_e3m2_to_e5m2(uint8_t* v, int tid) {
+  constexpr int NI = BN * D / 16 / 256;
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    v4i* ptr = reinterpret_cast<v4i*>(v + 16 * (tid + 256 * i));
+    v4i w = *ptr;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t u = (uint32_t)w[e];
+      w[e] = (int)((u & 0x1f1f1f1fu) | ((u & 0x20202020u) << 2));
+    }
+    *ptr = w;
+  }
+}
+
 // The lane index, recomputed where it is used (two VALU instructions the compiler cannot
 // merge with an earlier copy): addresses derived from it need no register across the loop.
 __device__ __forceinline__ int fresh_lane() {
@@ -1732,14 +1588,18 @@ __device__ __forceinline__ int fresh_lane() {
   return l;
 }
 
-template <int D, bool SOFTCAP, int PR, bool TRACE = false>
+// NOWS: the workspace-free form (mxfa_prefill): K read as E4M3 codes and widened to bf16 in
+// LDS by p3n_widen_k at the top of every block (one K stage), V read from the caller's array;
+// VE3: V is E3M2, rewritten in LDS as E5M2 (p3n_v_e3m2_to_e5m2), O scaled by 2^12.
+template <int D, bool SOFTCAP, int PR, bool TRACE = false, bool NOWS = false, bool VE3 = false>
 __device__ void prefill3_impl(const FaArgs& a) {
   using L = P3Lds<D>;
   constexpr int NW = P3Waves<D>::N;
   fp32_flush_denormals();   // pipe_softmax's R1 flush
-  constexpr bool K1 = p3_one_k_stage<D>();
+  constexpr bool K1 = NOWS || p3_one_k_stage<D>();
   __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
   __shared__ __attribute__((aligned(16))) uint8_t sKb1[K1 ? 16 : L::KB];
+  __shared__ __attribute__((aligned(16))) uint8_t sKs[NOWS ? (BN * D / 32 > 256 ? BN * D / 32 : 256) : 16];
   __shared__ __attribute__((aligned(256))) uint8_t sV0[L::V + L::SCB];   // 256-aligned: pv_parts' addresses
   __shared__ __attribute__((aligned(256))) uint8_t sV1[L::V + L::SCB];
 
@@ -1780,9 +1640,16 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const bool wave_live = qw0 < a.Sq;
 
   // V codes: the caller's E4M3 V, or its E4M3 copy (dense, Sk keys) when V is E3M2
-  const P3Src src = p3_src(a.kbf + (int64_t)bk * a.Sk * (2 * D),
-                           a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
-                           a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk, D);
+  const P3Src src = NOWS ? P3Src{} : p3_src(a.kbf + (int64_t)bk * a.Sk * (2 * D),
+                                           a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
+                                           a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk, D);
+  // workspace-free: the caller's K codes and scales, V and V scales (Skc keys apart), each
+  // resource ending at key Sk
+  const P3NSrc nsrc = !NOWS ? P3NSrc{}
+                            : P3NSrc{buf_rsrc(a.k, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D),
+                                     buf_rsrc(a.ks, (int64_t)bk * a.Skc * (D / 32), (int64_t)a.Sk * (D / 32)),
+                                     buf_rsrc(a.v, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D),
+                                     buf_rsrc(a.vs, (int64_t)bk * (a.Skc / 32) * D, (int64_t)(a.Sk / 32) * D)};
   const P3Lane pl = p3_lane<D, NW>(wave, lane);
   // loop-invariant operands in VGPRs at three waves per SIMD (D <= 128), in SGPRs at two (D =
   // 256: there an SGPR operand issues at the full-rate op's speed and saves the register)
@@ -1793,14 +1660,18 @@ __device__ void prefill3_impl(const FaArgs& a) {
   for (int dt = 0; dt < D / 32; dt++) o[dt] = (v16f){};
   float m = -INFINITY, l = 0.0f;
 
+  // the wave's rows end at or past Sq (or it has none): every block is masked
+  const bool edge_wave = __builtin_amdgcn_readfirstlane((qw0 + 31 >= a.Sq) || !wave_live);
   auto need_mask = [&](int j) {
     const int key0 = j * BN, key1 = key0 + BN - 1;
-    return (bool)__builtin_amdgcn_readfirstlane(
-        (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
-        (qw0 + 31 >= a.Sq) || !wave_live);
+    return edge_wave || (bool)__builtin_amdgcn_readfirstlane((key1 >= a.Sk) || (a.causal && key1 > wq_lo) ||
+                                                              (a.window > 0 && key0 + a.window <= wq_hi));
   };
 
-  if (j0 < j1) p3_dma<D, NW>(src, sKb0, sV0, j0 * BN, wave, pl);
+  if (j0 < j1) {
+    if constexpr (NOWS) p3n_dma<D>(nsrc, sKb0, sKs, sV0, j0 * BN, wave, lane, pl);
+    else p3_dma<D, NW>(src, sKb0, sV0, j0 * BN, wave, pl);
+  }
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
   __syncthreads();
 
@@ -1814,6 +1685,15 @@ __device__ void prefill3_impl(const FaArgs& a) {
     // nothing reads that stage) are issued between the score MFMAs of block j, or -- one K
     // stage -- once every wave has read K(j), while the MFMAs run
     v16f sc[BN / 32];
+    if constexpr (NOWS) {
+      // widen this block's K group of the wave (and rewrite an E3M2 V tile as E5M2), then
+      // let every wave see the whole tile
+      // (lane ids recomputed here: addresses held across the loop would not fit at D = 256)
+      p3n_widen_k<D>(sKb0, sKs, wave, fresh_lane());
+      if constexpr (VE3) p3n_v_e3m2_to_e5m2<D>(v_cur, 64 * wave + fresh_lane());
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+    }
     // D <= 128: the score MFMAs at raised wave priority, so that the SIMD's arbiter issues them
     // ahead of the other two workgroups' softmax VALU (about 1% faster on the S = 4096 GQA
     // prefill); D = 256 (two waves per SIMD) runs about 0.5% faster without it
@@ -1825,7 +1705,8 @@ __device__ void prefill3_impl(const FaArgs& a) {
     if constexpr (K1) {
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's K operand reads are done
       __builtin_amdgcn_s_barrier();
-      p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+      if constexpr (NOWS) p3n_dma<D>(nsrc, kb_dma, sKs, v_dma, (j + 1) * BN, wave, fresh_lane(), pl);
+      else p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
     } else {
       p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
       p3_dma_interleave<D>();
@@ -1852,7 +1733,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
     v8i pb;
     int psc[BN / 32];
     float corr;
-    pipe_softmax<SOFTCAP, PR>(m, l, sc, pb, psc, corr, c, -2.0f * a.cap_log2, a.cap_log2);
+    pipe_softmax<SOFTCAP, PR, D <= 128>(m, l, sc, pb, psc, corr, c, -2.0f * a.cap_log2, a.cap_log2);
     if constexpr (TRACE) {
       const float lrow = pair_sum(l);
       if (traced) {
@@ -1880,7 +1761,7 @@ __device__ void prefill3_impl(const FaArgs& a) {
         for (int i = 0; i < 16; i++) o[dt][i] *= corr;
     }
     // D <= 128: the PV addresses stay in registers (loop-invariant); D = 256 has no room
-    pv_parts<D, D == 256 ? 2 : 1>(o, v_cur, pb, psc, D == 256 ? fresh_lane() : lane);
+    pv_parts<D, D == 256 ? 2 : 1, VE3>(o, v_cur, pb, psc, D == 256 ? fresh_lane() : lane);
     __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);   // vmcnt(0) lgkmcnt(0): next stage landed
     __builtin_amdgcn_s_barrier();
   };
@@ -1890,12 +1771,16 @@ __device__ void prefill3_impl(const FaArgs& a) {
   }
 
   const float lt = pair_sum(l);
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  // (an E3M2 V read as E5M2 carries 2^-12: undone here, exactly)
+  const float inv = lt > 0.0f ? (VE3 ? 4096.0f : 1.0f) / lt : 0.0f;
   if constexpr (D >= 128 && !TRACE) {
-    // O through LDS (store_o_lds), in a private 8 KB slice of the K tiles, free after the
-    // loop's last barrier (96 -> 68 MB fetched and 161 -> 134 MB written on the S = 4096 GQA
-    // prefill)
-    float* const ldsw = reinterpret_cast<float*>(D == 256 ? sKb0 + wave * 8192 : (wave < 2 ? sKb0 : sKb1) + (wave & 1) * 8192);
+    // O through LDS (store_o_lds), in a private 8 KB slice of the K tiles (one K stage at D =
+    // 128: the V tiles for waves 2 and 3), free after the loop's last barrier (96 -> 68 MB
+    // fetched and 161 -> 134 MB written on the S = 4096 GQA prefill)
+    float* const ldsw = reinterpret_cast<float*>(
+        D == 256 ? sKb0 + wave * 8192
+        : K1     ? (wave < 2 ? sKb0 + wave * 8192 : wave == 2 ? sV0 : sV1)
+                 : (wave < 2 ? sKb0 : sKb1) + (wave & 1) * 8192);
     store_o_lds<D>(o, inv, ldsw, a.o + bh * a.Sq * D, qw0, a.Sq, lane);
   } else if (qvalid) {
     float* orow = a.o + (bh * a.Sq + qi) * D;
@@ -1926,6 +1811,29 @@ MXFA_PREFILL3(256, false, P_R1, mxfa_prefill3_d256)
 MXFA_PREFILL3(256, true, P_R1, mxfa_prefill3_d256_softcap)
 MXFA_PREFILL3(256, false, P_R2, mxfa_prefill3_d256_r2)
 MXFA_PREFILL3(256, true, P_R2, mxfa_prefill3_d256_softcap_r2)
+
+// Workspace-free prefill (mxfa_prefill) for D = 256 and for E3M2 V: K widened in LDS, E3M2 V
+// read as E5M2.  (D <= 128 with E4M3 V runs the software-pipelined kernel.)
+#define MXFA_PREFILL3N(D, SC, PR, VE3, NAME)                                                        \
+  extern "C" __global__ void __launch_bounds__(256, D == 256 ? 2 : 3) NAME(FaArgs a) {               \
+    prefill3_impl<D, SC, PR, false, true, VE3>(a);                                                   \
+  }
+MXFA_PREFILL3N(256, false, P_R1, false, mxfa_prefill3n_d256)
+MXFA_PREFILL3N(256, true, P_R1, false, mxfa_prefill3n_d256_softcap)
+MXFA_PREFILL3N(256, false, P_R2, false, mxfa_prefill3n_d256_r2)
+MXFA_PREFILL3N(256, true, P_R2, false, mxfa_prefill3n_d256_softcap_r2)
+MXFA_PREFILL3N(64, false, P_R1, true, mxfa_prefill3n_d64_e3m2)
+MXFA_PREFILL3N(128, false, P_R1, true, mxfa_prefill3n_d128_e3m2)
+MXFA_PREFILL3N(256, false, P_R1, true, mxfa_prefill3n_d256_e3m2)
+MXFA_PREFILL3N(64, true, P_R1, true, mxfa_prefill3n_d64_softcap_e3m2)
+MXFA_PREFILL3N(128, true, P_R1, true, mxfa_prefill3n_d128_softcap_e3m2)
+MXFA_PREFILL3N(256, true, P_R1, true, mxfa_prefill3n_d256_softcap_e3m2)
+MXFA_PREFILL3N(64, false, P_R2, true, mxfa_prefill3n_d64_r2_e3m2)
+MXFA_PREFILL3N(128, false, P_R2, true, mxfa_prefill3n_d128_r2_e3m2)
+MXFA_PREFILL3N(256, false, P_R2, true, mxfa_prefill3n_d256_r2_e3m2)
+MXFA_PREFILL3N(64, true, P_R2, true, mxfa_prefill3n_d64_softcap_r2_e3m2)
+MXFA_PREFILL3N(128, true, P_R2, true, mxfa_prefill3n_d128_softcap_r2_e3m2)
+MXFA_PREFILL3N(256, true, P_R2, true, mxfa_prefill3n_d256_softcap_r2_e3m2)
 
 // Stage trace of the same kernel (one workgroup; mxfa_prefill_trace).
 #define MXFA_PREFILL3_TRACE(D, SC, PR, NAME)                                                                  \
