@@ -11,6 +11,7 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -46,9 +47,6 @@ const char* const kKernelNames[] = {
     "mxfa_decode_d64_r2", "mxfa_decode_d128_r2",
     "mxfa_decode_d256_r2",     "mxfa_decode_d64_softcap_r2", "mxfa_decode_d128_softcap_r2",
     "mxfa_decode_d256_softcap_r2", "mxfa_gemm", "mxfa_gemm_ae3m2", "mxfa_gemm_be3m2", "mxfa_gemm_ae3m2_be3m2",
-    "mxfa_prefill_pipe_d64",   "mxfa_prefill_pipe_d128",  "mxfa_prefill_pipe_d64_softcap", "mxfa_prefill_pipe_d128_softcap",
-    "mxfa_prefill_pipe_d64_r2", "mxfa_prefill_pipe_d128_r2", "mxfa_prefill_pipe_d64_softcap_r2",
-    "mxfa_prefill_pipe_d128_softcap_r2",
     "mxfa_k_to_bf16",          "mxfa_prefill3_d64",       "mxfa_prefill3_d128",   "mxfa_prefill3_d64_softcap",
     "mxfa_prefill3_d128_softcap", "mxfa_prefill3_d64_r2", "mxfa_prefill3_d128_r2", "mxfa_prefill3_d64_softcap_r2",
     "mxfa_prefill3_d128_softcap_r2",
@@ -58,7 +56,10 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3_trace_d64_r2", "mxfa_prefill3_trace_d128_r2", "mxfa_prefill3_trace_d256_r2",
     "mxfa_prefill3_trace_d64_softcap_r2", "mxfa_prefill3_trace_d128_softcap_r2", "mxfa_prefill3_trace_d256_softcap_r2",
     "mxfa_gemm_dma",
-    "mxfa_prefill3n_d256", "mxfa_prefill3n_d256_softcap", "mxfa_prefill3n_d256_r2", "mxfa_prefill3n_d256_softcap_r2",
+    "mxfa_prefill3n_d64", "mxfa_prefill3n_d128", "mxfa_prefill3n_d256", "mxfa_prefill3n_d64_softcap",
+    "mxfa_prefill3n_d128_softcap", "mxfa_prefill3n_d256_softcap", "mxfa_prefill3n_d64_r2", "mxfa_prefill3n_d128_r2",
+    "mxfa_prefill3n_d256_r2", "mxfa_prefill3n_d64_softcap_r2", "mxfa_prefill3n_d128_softcap_r2",
+    "mxfa_prefill3n_d256_softcap_r2",
     "mxfa_prefill3n_d64_e3m2", "mxfa_prefill3n_d128_e3m2", "mxfa_prefill3n_d256_e3m2",
     "mxfa_prefill3n_d64_softcap_e3m2", "mxfa_prefill3n_d128_softcap_e3m2", "mxfa_prefill3n_d256_softcap_e3m2",
     "mxfa_prefill3n_d64_r2_e3m2", "mxfa_prefill3n_d128_r2_e3m2", "mxfa_prefill3n_d256_r2_e3m2",
@@ -467,6 +468,30 @@ FaArgs prefill_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* 
   return a;
 }
 
+// Wave-blocks (32 queries x 64 keys) of one launch of the prefill3 grid: every wave of a
+// workgroup walks the workgroup's key blocks [j0, j1) (the kernels' own loop bounds).
+int64_t prefill3_wave_blocks(const FaArgs& a, const mxfa_attn_params* p) {
+  const int nkb = (p->seq_k + 63) / 64;
+  int64_t per_group = 0;
+  for (int qblk = 0; qblk < a.n_qblk; qblk++) {
+    const int q0 = qblk * a.qpw, qmax = std::min(q0 + a.qpw, p->seq_q) - 1;
+    const int j0 = p->window > 0 ? std::max(0, p->q_pos0 + q0 - p->window + 1) / 64 : 0;
+    const int j1 = p->causal ? std::min(nkb, std::max(0, p->q_pos0 + qmax) / 64 + 1) : nkb;
+    per_group += 4 * std::max(0, j1 - j0);
+  }
+  return per_group * p->batch * p->num_kv_heads * (a.group / a.hpw);
+}
+
+// mxfa_prefill_ws widens K to bf16 once, into the workspace, by a pre-pass -- or leaves it to
+// the workspace-free kernel, whose workgroups widen each block they read in LDS: each K
+// element about 16 * wave_blocks / (B * Hkv * Sk) times.  Measured (same box): at 8.5 (MHA,
+// S = 2048) the in-LDS form is 3.4% faster; at 49 (Gemma shape) 2-4% and at 65 (GQA-4, S =
+// 4096) 6.5% slower.  Below 32 the call runs the workspace-free kernel (the workspace is
+// then not touched).
+bool prefill_ws_widens_in_lds(const FaArgs& a, const mxfa_attn_params* p) {
+  return 16 * prefill3_wave_blocks(a, p) < (int64_t)32 * p->batch * p->num_kv_heads * p->seq_k;
+}
+
 // Waves per workgroup of the workspace kernel (mxfa_prefill3_*).
 int prefill3_waves(const mxfa_attn_params*) { return 4; }
 
@@ -493,11 +518,8 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   dim3 grid;
   FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, 4, grid);
   void* args[] = {&a};
-  // D <= 128 with E4M3 V: the software-pipelined kernel (LDS-DMA staging, score MFMAs of
-  // the next block inside the softmax); D = 256 and E3M2 V: the workspace kernel's design in
-  // its workspace-free form (K widened to bf16 in LDS, E3M2 V read as E5M2).
-  if (p->head_dim <= 128 && p->v_fmt == MXFA_FMT_E4M3)
-    return launch(dm, kernel_name("prefill_pipe", p), grid, dim3(256), args, stream);
+  // the workspace kernel's design in its workspace-free form: K widened to bf16 in LDS, E3M2
+  // V read as E5M2
   return launch(dm, kernel_name("prefill3n", p, p->v_fmt == MXFA_FMT_E3M2), grid, dim3(256), args, stream);
 }
 
@@ -533,6 +555,10 @@ mxfa_status prefill_ws_impl(const mxfa_attn_params* p, const uint8_t* q, const u
   const int nw = prefill3_waves(p);
   dim3 grid;
   FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, nw, grid);
+  if (!tr && prefill_ws_widens_in_lds(a, p)) {
+    void* args[] = {&a};
+    return launch(dm, kernel_name("prefill3n", p, p->v_fmt == MXFA_FMT_E3M2), grid, dim3(256), args, stream);
+  }
   uint8_t* kbf = static_cast<uint8_t*>(workspace);
   uint8_t* vws = p->v_fmt == MXFA_FMT_E3M2 ? kbf + prefill3_kbf_bytes(p) : nullptr;
   a.kbf = kbf;

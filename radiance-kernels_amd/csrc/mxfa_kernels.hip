@@ -389,25 +389,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const uint8_t* base, 
   return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), 0, (int)(bytes > 0 ? bytes : 0), 0x00020000);
 }
 
-// The same loads through buffer resources over one (b, KV head)'s K, K scales, V and V
-// scales, built once per workgroup and bounded at Sk keys (a load at a key >= Sk reads
-// 0): the per-block cost is one offset add instead of building four resources (1.4%
-// faster at D = 128; at D = 256, one wave per SIMD, the per-block resources are faster).
-struct KvRsrc {
-  __amdgpu_buffer_rsrc_t k, ks, v, vs;
-};
-
-template <int D>
-__device__ __forceinline__ KvRsrc kv_rsrc(const uint8_t* kb, const uint8_t* ksb, const uint8_t* vb, const uint8_t* vsb,
-                                          int Sk) {
-  KvRsrc r;
-  r.k = buf_rsrc(kb, 0, (int64_t)Sk * D);
-  r.ks = buf_rsrc(ksb, 0, (int64_t)Sk * (D / 32));
-  r.v = buf_rsrc(vb, 0, (int64_t)Sk * D);
-  r.vs = buf_rsrc(vsb, 0, (int64_t)(Sk / 32) * D);
-  return r;
-}
-
 // Per-wave online-softmax state and O accumulator for 32 query columns.
 template <int D>
 struct WaveState {
@@ -710,30 +691,9 @@ __device__ __forceinline__ void load_q_split(v4i* qb, const uint8_t* qrow, const
 
 
 // ---------------------------------------------------------------------------
-// Prefill, D <= 128, E4M3 V: software-pipelined.  Iteration j runs the softmax and P
-// requant of key block j (VALU) with the score MFMAs of block j + 1 interleaved into the
-// same instruction stream, then the O rescale and the PV MFMAs of block j: the matrix
-// pipe works while the wave computes exponentials and codes, instead of the wave waiting
-// for its scores and then for its PV.  Staging goes through LDS DMA (buffer_load ... lds):
-// V codes and scales land in their padded tile directly, K codes and scales in an fp8
-// tile that the workgroup converts to the bf16 score operand one iteration later, so no
-// staging registers are held across iterations.  Stages (two of each, distinct LDS
-// objects so that the compiler's DMA waits stay at the barrier):
-//   iteration j reads   K_bf16(j+1) [scores of j+1]   V(j) [PV of j]   K8(j+2) [converted]
-//               writes  K_bf16(j+2)                    V(j+1) (DMA)     K8(j+3) (DMA)
-// One barrier per iteration.
+// LDS helpers of the prefill kernels: the V tile swizzle, LDS addresses, LDS DMA.
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
-
-template <int D> struct PipeLds {
-  static constexpr int KPB = 2 * D + 16;          // bf16 K row pitch (bytes)
-  static constexpr int KB = BN * KPB;             // bf16 K tile
-  static constexpr int K8 = BN * D;               // fp8 K tile, rows contiguous (DMA)
-  static constexpr int V = BN * D;                // V tile, rows of D bytes, 16-byte chunks swizzled
-  static constexpr int SCB = 256;                // K scales [BN][D/32] or V scales [BN/32][D] (2D bytes),
-                                                  // in a 256-byte slot: one dword DMA of 64 lanes
-  static constexpr int NDMA = BN * D / 1024;      // DMA instructions per K8 or V tile
-};
 
 // 16-byte chunk c of V key row `key` sits at chunk c ^ vsw(key) of its row: the
 // ds_read_b64_tr_b8 reads of the PV operand (16 keys x 32 bytes per instruction) then hit
@@ -760,109 +720,6 @@ __device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds_b
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_addr(lds_base), 2, voff, soff, 0, 0);
 }
 
-// The DMA instructions of one key block: fp8 K (do_k) into k8, V (do_v) into v; each wave
-// issues instructions wave, wave + 4, ... of each tile, wave 2 the K scales and wave 3 the
-// V scales.  Key rows >= Sk read 0 (buffer resources bounded at Sk).
-template <int D>
-__device__ __forceinline__ void pipe_dma(const KvRsrc& rs, uint8_t* k8, uint8_t* v, int key0, int wave, int lane,
-                                         bool do_k, bool do_v) {
-  using L = PipeLds<D>;
-  constexpr int RPI = 1024 / D;                    // V rows per DMA instruction
-#pragma unroll
-  for (int m = 0; m < L::NDMA / NWAVE; m++) {
-    const int i = wave + NWAVE * m;
-    if (do_k) dma_lds<16>(rs.k, k8 + i * 1024, key0 * D + i * 1024 + lane * 16);
-    if (do_v) {
-      const int row = i * RPI + lane / (D / 16), pos = lane % (D / 16);
-      dma_lds<16>(rs.v, v + i * 1024, (key0 + row) * D + ((pos ^ vsw<D>(row)) << 4));
-    }
-  }
-  // scales: one dword per lane (an LDS DMA writes its lanes 4 bytes apart below 16-byte
-  // loads); at D = 64 the upper 32 lanes carry the next block's scales, unused
-  if (do_k && wave == 2) dma_lds<4>(rs.ks, k8 + L::K8, key0 * (D / 32) + lane * 4);
-  if (do_v && wave == 3) dma_lds<4>(rs.vs, v + L::V, (key0 / 32) * D + lane * 4);
-}
-
-// fp8 K tile + scales (LDS) -> bf16 K tile (LDS), exact; 16-byte chunks dealt to threads.
-// In two halves: the LDS reads (issued early), then the converts and stores (later, when
-// the reads have landed), so the wave never waits on them.
-template <int D> struct ConvRegs {
-  static constexpr int N = BN * D / 16 / (NWAVE * 64);   // chunks per thread
-  v4i x[N];
-  uint32_t sc[N];
-};
-
-template <int D>
-__device__ __forceinline__ void pipe_convert_load(ConvRegs<D>& cr, const uint8_t* k8, int tid) {
-  using L = PipeLds<D>;
-#pragma unroll
-  for (int m = 0; m < ConvRegs<D>::N; m++) {
-    const int c = tid + m * NWAVE * 64;
-    const int key = c / (D / 16), col = c % (D / 16);
-    cr.x[m] = *reinterpret_cast<const v4i*>(k8 + c * 16);
-    cr.sc[m] = k8[L::K8 + key * (D / 32) + col / 2];
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void pipe_convert_store(const ConvRegs<D>& cr, uint8_t* kb, int tid) {
-  using L = PipeLds<D>;
-#pragma unroll
-  for (int m = 0; m < ConvRegs<D>::N; m++) {
-    const int c = tid + m * NWAVE * 64;
-    const int key = c / (D / 16), col = c % (D / 16);
-    const float sc = e8m0_as_float(cr.sc[m]);
-    const v4i b0 = fp8x8_to_bf16x8((uint32_t)cr.x[m][0], (uint32_t)cr.x[m][1], sc);
-    const v4i b1 = fp8x8_to_bf16x8((uint32_t)cr.x[m][2], (uint32_t)cr.x[m][3], sc);
-    *reinterpret_cast<v4i*>(kb + key * L::KPB + col * 32) = b0;
-    *reinterpret_cast<v4i*>(kb + key * L::KPB + col * 32 + 16) = b1;
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void pipe_convert_k(const uint8_t* k8, uint8_t* kb, int tid) {
-  ConvRegs<D> cr;
-  pipe_convert_load<D>(cr, k8, tid);
-  pipe_convert_store<D>(cr, kb, tid);
-}
-
-// Scores of one key block from the bf16 K tile: S^T tile t covers keys 32t .. 32t+31.
-// The two tiles' MFMA chains alternate (t0 k0, t1 k0, t0 k1, ...), so each MFMA depends on
-// the one issued two before it.
-template <int D>
-__device__ __forceinline__ void pipe_qk(v16f (&s)[BN / 32], const v4i* qb, const uint8_t* kb, int lane) {
-  constexpr int KPB = PipeLds<D>::KPB;
-  const int r = lane & 31, h = lane >> 5;
-  const uint8_t* krow = kb + r * KPB + 16 * h;
-#pragma unroll
-  for (int t = 0; t < BN / 32; t++) s[t] = (v16f){};
-#pragma unroll
-  for (int kk = 0; kk < D / 16; kk++)
-#pragma unroll
-    for (int t = 0; t < BN / 32; t++)
-      s[t] = mfma_bf16(*reinterpret_cast<const v4i*>(krow + t * 32 * KPB + 32 * kk), qb[kk], s[t]);
-}
-
-// Instruction order of the score/softmax region: per score MFMA, its K operand read, then
-// VALU work, the MFMA, more VALU -- the MFMAs run in the matrix pipe while the wave
-// issues the softmax, and no MFMA waits on its predecessor in the same chain.
-// RPM LDS reads per MFMA after the first AHEAD: the score operands AHEAD MFMAs ahead, then the
-// PV operands and the conversion reads of the same region.
-template <int D, int VPM, int AHEAD, int RPM>
-__device__ __forceinline__ void pipe_interleave() {
-  constexpr int NM = D / 16 * (BN / 32);
-  __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);     // first LDS reads
-#pragma unroll
-  for (int k = 0; k < NM; k++) {
-    __builtin_amdgcn_sched_group_barrier(0x002, VPM / 2, 0); // VALU
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA k
-    __builtin_amdgcn_sched_group_barrier(0x002, VPM - VPM / 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);     // LDS reads
-  }
-}
-
-// Softmax and P requant of one block's scores (in place: s holds the scores, masked and
-// capped): updates m and l, returns the PV operand codes and scales and the O correction.
 // max(a, b) without the canonicalizing maxes fmaxf adds on operands the compiler cannot prove
 // canonical (MFMA results, cross-lane swaps): IEEE maximum (v_maximum3_f32 on gfx950; a NaN
 // score, possible only from NaN operand codes, propagates instead of being dropped).
@@ -1034,42 +891,6 @@ __device__ __forceinline__ void pipe_mask(v16f (&s)[BN / 32], int key0, int klo,
     }
 }
 
-// PV operands of one block from the V tile: V^T through ds_read_b64_tr_b8 (byte t of read q:
-// key 32*(q/2) + 16*(q%2) + kl, d = 32*dt + lane%32 after the transpose; the key bits the
-// swizzle uses are those of kl) and the V scale of each d tile.
-template <int D> struct PvRegs {
-  v8i va[D / 32];
-  int vs[D / 32];
-};
-
-template <int D>
-__device__ __forceinline__ void pipe_pv_load(PvRegs<D>& pr, const uint8_t* sv, int lane) {
-  const int r = lane & 31, h = lane >> 5;
-  const int l16 = lane & 15, g16 = lane >> 4;
-  const int t8 = l16 >> 1;
-  const int kl = 8 * (t8 >> 2) + 4 * h + (t8 & 3);
-  const int sg = (g16 & 1) ^ vsw<D>(kl);
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) {
-    const uint8_t* base = sv + kl * D + (((2 * dt) ^ sg) << 4) + 8 * (l16 & 1);
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + (32 * (q >> 1) + 16 * (q & 1)) * D));
-      pr.va[dt][2 * q] = rv[0];
-      pr.va[dt][2 * q + 1] = rv[1];
-    }
-    pr.vs[dt] = sv[PipeLds<D>::V + h * D + dt * 32 + r];
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void pipe_pv(v16f (&o)[D / 32], const PvRegs<D>& pr, const v8i& pb,
-                                        const int (&psc)[BN / 32], int lane) {
-  const int pscale = psc[lane >> 5];
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) o[dt] = mfma_mx(pr.va[dt], pb, o[dt], pr.vs[dt], pscale);
-}
-
 // PV of one block in NP parts of D / NP columns: the operand registers of one part at a time
 // (D = 256 at two waves per SIMD: 32 registers instead of 64).
 template <int D, int NP, bool V5 = false>
@@ -1104,7 +925,7 @@ __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, c
         va[u][2 * q] = rv[0];
         va[u][2 * q + 1] = rv[1];
       }
-      vs[u] = sv[PipeLds<D>::V + h * D + dt * 32 + r];
+      vs[u] = sv[BN * D + h * D + dt * 32 + r];   // the V scales follow the BN x D codes
     }
 #pragma unroll
     for (int u = 0; u < NT; u++)
@@ -1147,185 +968,6 @@ __device__ __forceinline__ void store_o_lds(const v16f (&o)[D / 32], float inv, 
   }
 }
 
-template <int D, bool SOFTCAP, int PR>
-__device__ void prefill_pipe_impl(const FaArgs& a) {
-  using L = PipeLds<D>;
-  fp32_flush_denormals();   // pipe_softmax's R1 flush
-  __shared__ __attribute__((aligned(16))) uint8_t sKb0[L::KB];
-  __shared__ __attribute__((aligned(16))) uint8_t sKb1[L::KB];
-  __shared__ __attribute__((aligned(16))) uint8_t sK8[3][L::K8 + L::SCB];   // K8(j) in sK8[j % 3]
-  __shared__ __attribute__((aligned(16))) uint8_t sV0[L::V + L::SCB];
-  __shared__ __attribute__((aligned(16))) uint8_t sV1[L::V + L::SCB];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 31, h = lane >> 5;
-  // workgroup -> work item: contiguous ranges per XCD, heads interleaved, longest first
-  // (the same map as prefill3_impl)
-  const int nwg = (int)(gridDim.x * gridDim.y);
-  const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
-  const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
-  const int start_x = xcd * per + min(xcd, rem), cnt_x = per + (xcd < rem ? 1 : 0);
-  const int li = lin >> 3;
-  const int nh_x = cnt_x / a.n_qblk;
-  const bool whole_heads = start_x % a.n_qblk == 0 && cnt_x % a.n_qblk == 0;
-  const int item = start_x + (whole_heads ? (li % nh_x) * a.n_qblk + li / nh_x : li);
-  const int qx = item % a.n_qblk, qy = item / a.n_qblk;
-  const int qblk = a.causal ? (a.n_qblk - 1 - qx) : qx;
-  const int chunks = a.group / a.hpw;
-  const int bk = qy / chunks;
-  const int hc = qy % chunks;
-  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
-  const int head = kvh * a.group + hc * a.hpw + (wave % a.hpw);
-  const int q0 = qblk * a.qpw;
-  const int qw0 = q0 + (wave / a.hpw) * 32;
-  const int qi = qw0 + r;
-  const bool qvalid = qi < a.Sq;
-  const int qpos = a.q_pos0 + qi;
-
-  const int64_t bh = (int64_t)b * a.Hq + head;
-  v4i qb[D / 16];
-  load_q<D>(qb, a.q + (bh * a.Sq + qi) * D, a.qs + (bh * a.Sq + qi) * (D / 32), qvalid, h);
-  int klo, khi;
-  key_limits(a, qpos, qvalid, klo, khi);
-
-  const int qmax_wg = min(q0 + a.qpw, a.Sq) - 1;
-  const int nkb = (a.Sk + BN - 1) / BN;
-  int j0 = 0, j1 = nkb;
-  if (a.window > 0) j0 = max(0, a.q_pos0 + q0 - a.window + 1) / BN;
-  if (a.causal) j1 = min(nkb, max(0, a.q_pos0 + qmax_wg) / BN + 1);
-  const int wq_lo = a.q_pos0 + qw0, wq_hi = a.q_pos0 + min(qw0 + 31, a.Sq - 1);
-  const bool wave_live = qw0 < a.Sq;
-
-  const KvRsrc rs = kv_rsrc<D>(a.k + (int64_t)bk * a.Skc * D, a.ks + (int64_t)bk * a.Skc * (D / 32),
-                               a.v + (int64_t)bk * a.Skc * D, a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk);
-  const float c = SOFTCAP ? 1.0f : in_vgpr(a.c_log2);
-
-  v16f o[D / 32];
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) o[dt] = (v16f){};
-  float m = -INFINITY, l = 0.0f;
-  v16f sa[BN / 32], sb[BN / 32];
-
-  // the mask is needed on blocks holding keys outside some row's visible range
-  auto need_mask = [&](int j) {
-    const int key0 = j * BN, key1 = key0 + BN - 1;
-    return (bool)__builtin_amdgcn_readfirstlane(
-        (key1 >= a.Sk) || (a.causal && key1 > wq_lo) || (a.window > 0 && key0 + a.window <= wq_hi) ||
-        (qw0 + 31 >= a.Sq) || !wave_live);
-  };
-
-  // Waits: the DMAs of iteration j are issued V(j+1) first, then K8(j+4); the end of the
-  // iteration waits until only this wave's K8(j+4) instructions may be outstanding (loads
-  // complete in order), so V(j+1) -- needed next -- and K8(j+3) -- converted next -- have
-  // landed, and K8(j+4) keeps a whole iteration more.
-  auto k8slot = [&](int j) { return sK8[j % 3]; };
-  if (j0 < j1) {
-    // prologue: K(j0), K(j0+1) converted, V(j0) resident, K8(j0+2) landed, K8(j0+3) in
-    // flight; the scores of block j0
-    pipe_dma<D>(rs, k8slot(j0), sV0, j0 * BN, wave, lane, true, true);
-    if (j0 + 1 < j1) pipe_dma<D>(rs, k8slot(j0 + 1), sV1, (j0 + 1) * BN, wave, lane, true, false);
-    if (j0 + 2 < j1) pipe_dma<D>(rs, k8slot(j0 + 2), sV1, (j0 + 2) * BN, wave, lane, true, false);
-    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
-    __syncthreads();
-    pipe_convert_k<D>(k8slot(j0), sKb0, tid);
-    if (j0 + 1 < j1) pipe_convert_k<D>(k8slot(j0 + 1), sKb1, tid);
-    __syncthreads();
-    if (j0 + 3 < j1) pipe_dma<D>(rs, k8slot(j0 + 3), sV1, (j0 + 3) * BN, wave, lane, true, false);
-    pipe_qk<D>(sa, qb, sKb0, lane);
-    __syncthreads();
-  }
-
-  // one iteration; ST = stage of block j (compile time), scur/snext its and the next
-  // block's score registers
-  auto step = [&](auto stc, int j, v16f (&scur)[BN / 32], v16f (&snext)[BN / 32]) {
-    constexpr int ST = decltype(stc)::value;
-    uint8_t* kb_next = ST ? sKb0 : sKb1;      // K_bf16(j+1)
-    uint8_t* kb_conv = ST ? sKb1 : sKb0;      // K_bf16(j+2) <- K8(j+2)
-    uint8_t* v_cur = ST ? sV1 : sV0;          // V(j)
-    uint8_t* v_dma = ST ? sV0 : sV1;          // V(j+1)
-    const int key0 = j * BN;
-    const bool k8_next = j + 4 < j1;
-    if (j + 1 < j1) pipe_dma<D>(rs, nullptr, v_dma, (j + 1) * BN, wave, lane, false, true);
-    if (k8_next) pipe_dma<D>(rs, k8slot(j + 4), nullptr, (j + 4) * BN, wave, lane, true, false);
-    // K(j+2) is converted unconditionally (no branch inside the region below): past the last
-    // block the slot holds stale codes, whose conversion nothing reads
-    ConvRegs<D> cr;
-    pipe_convert_load<D>(cr, k8slot(j + 2), tid);
-    // scores of block j: softcap, mask
-    pipe_scores<SOFTCAP>(scur, a);
-    if (need_mask(j)) {
-      __asm__ volatile("");
-      pipe_mask<SOFTCAP>(scur, key0, klo, khi, h);
-    }
-    // scores of block j+1 (MFMA) with the softmax and requant of block j (VALU); the
-    // conversion of K(j+2) and the PV operand reads of block j inside the same region
-    pipe_qk<D>(snext, qb, kb_next, lane);
-    v8i pb;
-    int psc[BN / 32];
-    float corr;
-    pipe_softmax<SOFTCAP, PR>(m, l, scur, pb, psc, corr, c, -2.0f * a.cap_log2, a.cap_log2);
-    pipe_convert_store<D>(cr, kb_conv, tid);
-    PvRegs<D> pr;
-    pipe_pv_load<D>(pr, v_cur, lane);
-    // the codes and the row sum are complete here (not sunk below the rescale branch), so
-    // the whole softmax shares the region with the score MFMAs
-    __asm__ volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]), "v"(pb[4]), "v"(pb[5]), "v"(pb[6]),
-                     "v"(pb[7]), "v"(l));
-    pipe_interleave<D, 16, 3, 2>();
-    if (__any(corr != 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) o[dt][i] *= corr;
-    }
-    pipe_pv<D>(o, pr, pb, psc, lane);
-    // vmcnt(K8 instructions of this wave) lgkmcnt(0): V(j+1), K8(j+3) and the LDS stores
-    // have landed (wave 2 issues one K8 instruction more, the K scales: it waits a little
-    // longer than it has to)
-    if (k8_next)
-      __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | (L::NDMA / NWAVE));
-    else
-      __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);
-    __builtin_amdgcn_s_barrier();
-  };
-  for (int j = j0; j < j1; j += 2) {
-    step(std::integral_constant<int, 0>{}, j, sa, sb);
-    if (j + 1 < j1) step(std::integral_constant<int, 1>{}, j + 1, sb, sa);
-  }
-
-  // finalize: O = O / l (0 where no key was visible)
-  const float lt = pair_sum(l);
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if constexpr (D >= 128) {
-    // O through LDS (store_o_lds) in a private 8 KB slice of the bf16 K tiles, once no DMA,
-    // conversion or read of any wave is in flight
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    float* const ldsw = reinterpret_cast<float*>((wave < 2 ? sKb0 : sKb1) + (wave & 1) * 8192);
-    store_o_lds<D>(o, inv, ldsw, a.o + bh * a.Sq * D, qw0, a.Sq, lane);
-  } else if (qvalid) {
-    float* orow = a.o + (bh * a.Sq + qi) * D;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const float4 w = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                                     o[dt][4 * g + 3] * inv);
-        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * h) = w;
-      }
-  }
-}
-
-#define MXFA_PREFILL_PIPE(D, SC, PR, NAME) \
-  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { prefill_pipe_impl<D, SC, PR>(a); }
-MXFA_PREFILL_PIPE(64, false, P_R1, mxfa_prefill_pipe_d64)
-MXFA_PREFILL_PIPE(128, false, P_R1, mxfa_prefill_pipe_d128)
-MXFA_PREFILL_PIPE(64, true, P_R1, mxfa_prefill_pipe_d64_softcap)
-MXFA_PREFILL_PIPE(128, true, P_R1, mxfa_prefill_pipe_d128_softcap)
-MXFA_PREFILL_PIPE(64, false, P_R2, mxfa_prefill_pipe_d64_r2)
-MXFA_PREFILL_PIPE(128, false, P_R2, mxfa_prefill_pipe_d128_r2)
-MXFA_PREFILL_PIPE(64, true, P_R2, mxfa_prefill_pipe_d64_softcap_r2)
-MXFA_PREFILL_PIPE(128, true, P_R2, mxfa_prefill_pipe_d128_softcap_r2)
 
 // ---------------------------------------------------------------------------
 // Prefill at three waves per SIMD (D <= 128, E4M3 V).  The MX K operand is dequantized
@@ -1400,7 +1042,7 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_k_to_bf16(const uint8_t* 
 template <int D> struct P3Lds {
   static constexpr int KB = BN * 2 * D;           // bf16 K tile
   static constexpr int KDMA = KB / 1024;          // DMA instructions per K tile
-  static constexpr int V = BN * D;                // V tile (swizzled as PipeLds)
+  static constexpr int V = BN * D;                // V tile (16-byte chunks swizzled by vsw)
   static constexpr int VDMA = V / 1024;
   static constexpr int SCB = 2 * D > 256 ? 2 * D : 256;   // V scales [BN / 32][D], dword DMA
 };
@@ -1812,15 +1454,23 @@ MXFA_PREFILL3(256, true, P_R1, mxfa_prefill3_d256_softcap)
 MXFA_PREFILL3(256, false, P_R2, mxfa_prefill3_d256_r2)
 MXFA_PREFILL3(256, true, P_R2, mxfa_prefill3_d256_softcap_r2)
 
-// Workspace-free prefill (mxfa_prefill) for D = 256 and for E3M2 V: K widened in LDS, E3M2 V
-// read as E5M2.  (D <= 128 with E4M3 V runs the software-pipelined kernel.)
+// Workspace-free prefill (mxfa_prefill, and mxfa_prefill_ws where widening K per workgroup
+// costs less than the pre-pass): K widened in LDS, E3M2 V read as E5M2.
 #define MXFA_PREFILL3N(D, SC, PR, VE3, NAME)                                                        \
   extern "C" __global__ void __launch_bounds__(256, D == 256 ? 2 : 3) NAME(FaArgs a) {               \
     prefill3_impl<D, SC, PR, false, true, VE3>(a);                                                   \
   }
+MXFA_PREFILL3N(64, false, P_R1, false, mxfa_prefill3n_d64)
+MXFA_PREFILL3N(128, false, P_R1, false, mxfa_prefill3n_d128)
 MXFA_PREFILL3N(256, false, P_R1, false, mxfa_prefill3n_d256)
+MXFA_PREFILL3N(64, true, P_R1, false, mxfa_prefill3n_d64_softcap)
+MXFA_PREFILL3N(128, true, P_R1, false, mxfa_prefill3n_d128_softcap)
 MXFA_PREFILL3N(256, true, P_R1, false, mxfa_prefill3n_d256_softcap)
+MXFA_PREFILL3N(64, false, P_R2, false, mxfa_prefill3n_d64_r2)
+MXFA_PREFILL3N(128, false, P_R2, false, mxfa_prefill3n_d128_r2)
 MXFA_PREFILL3N(256, false, P_R2, false, mxfa_prefill3n_d256_r2)
+MXFA_PREFILL3N(64, true, P_R2, false, mxfa_prefill3n_d64_softcap_r2)
+MXFA_PREFILL3N(128, true, P_R2, false, mxfa_prefill3n_d128_softcap_r2)
 MXFA_PREFILL3N(256, true, P_R2, false, mxfa_prefill3n_d256_softcap_r2)
 MXFA_PREFILL3N(64, false, P_R1, true, mxfa_prefill3n_d64_e3m2)
 MXFA_PREFILL3N(128, false, P_R1, true, mxfa_prefill3n_d128_e3m2)

@@ -33,8 +33,8 @@ def test_code_object_present_and_for_gfx950():
     assert b"gfx950" in data
     for k in ("mxfa_prefill3n_d256", "mxfa_decode_d128", "mxfa_quant_rows_e4m3", "mxfa_softmax_requant_rows",
               "mxfa_prefill3n_d128_softcap_r2_e3m2", "mxfa_decode_d64_softcap_r2", "mxfa_decode_scratch",
-              "mxfa_k_to_bf16", "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill_pipe_d128",
-              "mxfa_prefill3_d256_softcap"):
+              "mxfa_k_to_bf16", "mxfa_prefill3_d128", "mxfa_prefill3_d64_softcap_r2", "mxfa_prefill3n_d128",
+              "mxfa_prefill3_d256_softcap", "mxfa_prefill3n_d64"):
         assert k.encode() in data
 
 

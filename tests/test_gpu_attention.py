@@ -30,10 +30,10 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
                          v_fmt=v_fmt, p_rule=p_rule)
     out = torch.full((B, Hq, Sq, D), float("nan"), dtype=torch.float32, device=DEV)
     mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out)
-    # the workspace-free kernels (mxfa_prefill): with E4M3 V the same arithmetic in the same
-    # order as the workspace kernel (bit-identical O: D <= 128 the pipelined kernel, D = 256 K
-    # widened in LDS); with E3M2 V the PV MFMA reads V as E5M2 (O within a few ulps of the
-    # workspace kernel's), checked against the oracle
+    # the workspace-free kernel (mxfa_prefill: K widened to bf16 in LDS): with E4M3 V the same
+    # arithmetic in the same order as the workspace kernel (bit-identical O); with E3M2 V the
+    # PV MFMA reads V as E5M2 (O within a few ulps of the workspace kernel's), checked against
+    # the oracle
     out_nw = torch.full_like(out, float("nan"))
     mxfa.prefill(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"], out=out_nw, workspace=False)
     torch.cuda.synchronize()

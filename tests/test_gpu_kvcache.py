@@ -129,7 +129,7 @@ def test_prefill_in_place_on_strided_cache(D, fmt):
     """Prefill with several query tiles (Sq > 32) over caches whose rows are kv_stride >
     seq_k apart, the rows past seq_k holding garbage codes: the workspace prefill (its
     pre-pass reads K -- and E3M2 V -- at the cache stride) and the workspace-free kernel
-    (pipelined kernel for D <= 128 with E4M3 V, K widened in LDS otherwise) give O bit for bit equal
+    (K codes and scales read at the cache stride, widened in LDS) give O bit for bit equal
     to the same calls on dense copies of the first seq_k keys, within tolerance of the oracle."""
     B, Hq, Hkv, Sq, Sk, Lcap = 2, 4, 2, 96, 160, 256
     rng = np.random.default_rng(430 + D + 7 * fmt)
