@@ -111,20 +111,24 @@ mxfa_status mxfa_quantize_cols(const float *x, int64_t mats, int32_t rows, int32
 
 /* Prefill / full attention.  Replaces fa_entry + mu_schedule of the reference FA
  * kernels (kernels/flash_attention_mx_gqa/kernel.cpp:91-191,
- * kernels/flash_attention_mx_gemma/kernel.cpp:124-213). */
+ * kernels/flash_attention_mx_gemma/kernel.cpp:124-213).  Needs no workspace: every workgroup
+ * widens the K blocks it reads to bf16 in LDS (exact), and an E3M2 V tile is read by the PV
+ * MFMA as E5M2 (the same bits, sign moved; O rescaled by 2^12, exact).  Three 4-wave
+ * workgroups per CU for head_dim <= 128, two for 256. */
 mxfa_status mxfa_prefill(const mxfa_attn_params *p,
                          const uint8_t *q, const uint8_t *q_sc,
                          const uint8_t *k, const uint8_t *k_sc,
                          const uint8_t *v, const uint8_t *v_sc,
                          float *o, void *stream);
 
-/* Prefill with a caller workspace, the faster path for every shape.  A first launch writes the
- * bf16 value of every K element (E4M3 code x 2^(scale - 127), exact in bf16) and, for E3M2 V,
- * the E4M3 code of every V element (the same value) into the workspace; the attention kernel
- * then streams those copies into LDS by DMA: three 4-wave workgroups per CU for head_dim <= 128,
- * two (two waves per SIMD) for head_dim 256.  Same inputs, outputs and O as
- * mxfa_prefill within the tolerance of the reference's algorithm (bit-identical to it for
- * head_dim <= 128 with E4M3 V, where both run the same arithmetic in the same order).
+/* Prefill with a caller workspace.  A first launch writes the bf16 value of every K element
+ * (E4M3 code x 2^(scale - 127), exact in bf16) and, for E3M2 V, the E4M3 code of every V
+ * element (the same value) into the workspace; the attention kernel then streams those copies
+ * into LDS by DMA.  Where widening K in every workgroup costs less than one copy per call
+ * (about 16 * wave-blocks < 32 * batch * num_kv_heads * seq_k, e.g. one query head per KV
+ * head), the call runs mxfa_prefill's kernel instead and leaves the workspace untouched.  Same
+ * inputs, outputs and O as mxfa_prefill (bit-identical with E4M3 V, where both run the same
+ * arithmetic in the same order; within a few ulps with E3M2 V).
  * *workspace_bytes = batch * num_kv_heads * seq_k * head_dim * (2, or 3 with E3M2 V).  A
  * workspace smaller than the plan is MXFA_ERR_WORKSPACE.
  * Replaces the same reference entry point as mxfa_prefill (kernels/flash_attention_mx_gqa/
