@@ -50,7 +50,7 @@ def make_prefill(torch, mxfa, c, seed=1):
     V = torch.empty_like(K)
     for i, X in enumerate((Q, K, V)):
         mxfa.fill_normal(X, seed * 3 + i, c["outlier_p"], 20.0)
-    vf = mxfa.FMT_E3M2 if c.get("v_e3m2") else mxfa.FMT_E4M3
+    vf = c.get("v_fmt", mxfa.FMT_E3M2 if c.get("v_e3m2") else mxfa.FMT_E4M3)
     q, qs = mxfa.quantize_rows(Q)
     k, ks = mxfa.quantize_rows(K)
     v, vs = mxfa.quantize_cols(V, vf)
@@ -71,13 +71,13 @@ def bench_other_configs(torch, mxfa, args):
         ms = time_calls(torch, lambda: mxfa.prefill(p, *ops, out=out, workspace=ws), max(20, args.steps // 4),
                         args.warmup)
         flops = mxfa.attention_flops(p)
-        vbytes = ops[4].numel() * (0.75 if c.get("v_e3m2") else 1.0)
+        vbytes = ops[4].numel() * (0.75 if p.v_fmt == mxfa.FMT_E3M2 else 1.0)   # block-packed: 6 bits already
         nbytes = sum(t.numel() for t in (ops[0], ops[1], ops[2], ops[3], ops[5])) + vbytes + out.numel() * 4
         t = ms * 1e-3
         frac = max(flops / (MXFP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) / t
         res[name] = {"shape": f"B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} S={c['S']} D={c['D']}"
                               + (" causal" if c["causal"] else "") + (f" window={c['window']}" if c.get("window") else "")
-                              + (f" softcap={c['softcap']}" if c.get("softcap") else "") + (" V=E3M2" if c.get("v_e3m2") else ""),
+                              + (f" softcap={c['softcap']}" if c.get("softcap") else "") + {mxfa.FMT_E3M2: " V=E3M2", mxfa.FMT_E3M2_BLK: " V=E3M2 block-packed"}.get(p.v_fmt, ""),
                      "ms_per_call": round(ms, 4), "tflops": round(flops / t / 1e12, 1),
                      "gflop": round(flops / 1e9, 3), "mb": round(nbytes / 1e6, 1), "roofline_frac": round(frac, 4)}
         del ops, out, ws

@@ -53,7 +53,16 @@ typedef enum {
   MXFA_ERR_WORKSPACE = 5      /* workspace missing or too small */
 } mxfa_status;
 
-typedef enum { MXFA_FMT_E4M3 = 0, MXFA_FMT_E3M2 = 1 } mxfa_fmt;
+/* Element formats.  E4M3 and E3M2 hold one code per byte (E3M2 in the low 6 bits).
+ * MXFA_FMT_E3M2_BLK is E3M2 packed per MX block, for V only (mxfa_quantize_cols,
+ * mxfa_kv_append, mxfa_prefill, mxfa_prefill_ws): the 32 codes of one column's 32-row block
+ * are 24 bytes, read as one 192-bit little-endian integer of 6-bit fields: row 8g + 4a + b
+ * of the block (g < 4, a < 2, b < 4) in field 16a + 4g + b, i.e. bits 6f .. 6f+5 (the first 12
+ * bytes hold rows 0-3, 8-11, 16-19, 24-27, the last 12 rows 4-7, 12-15, 20-23, 28-31).  Blocks
+ * laid out [mats][rows/32][cols][24] (for V: [B][Hkv][kv_stride/32][D][24]).  That is the
+ * gfx950 scaled MFMA's fp6 operand in the key order of the kernels' P operand, so the
+ * attention kernels copy V into LDS as it is.  Same values and scales as MXFA_FMT_E3M2. */
+typedef enum { MXFA_FMT_E4M3 = 0, MXFA_FMT_E3M2 = 1, MXFA_FMT_E3M2_BLK = 2 } mxfa_fmt;
 
 /* Requant rule of the probabilities P (the PV operand).
  *  MXFA_P_R1: lib/golden's block-32 rule (lib/golden/mx_golden.cpp:146-190): scale
@@ -102,7 +111,8 @@ mxfa_status mxfa_quantize_rows_r4(const float *x, int64_t rows, int32_t cols,
                                   uint8_t *codes, uint8_t *scales, void *stream);
 
 /* 32-blocks along the rows of each of `mats` rows x cols matrices (V, KV-cache V).
- * codes [mats][rows][cols], scales [mats][rows/32][cols]; rows % 32 == 0, cols % 4 == 0.
+ * codes [mats][rows][cols] (MXFA_FMT_E3M2_BLK: [mats][rows/32][cols][24]),
+ * scales [mats][rows/32][cols]; rows % 32 == 0, cols % 4 == 0.
  * Replaces mx_quantize_cols(V.t()) of fa_gen_data.py:103-104. */
 mxfa_status mxfa_quantize_cols(const float *x, int64_t mats, int32_t rows, int32_t cols, mxfa_fmt fmt,
                                uint8_t *codes, uint8_t *scales, void *stream);
@@ -112,8 +122,9 @@ mxfa_status mxfa_quantize_cols(const float *x, int64_t mats, int32_t rows, int32
 /* Prefill / full attention.  Replaces fa_entry + mu_schedule of the reference FA
  * kernels (kernels/flash_attention_mx_gqa/kernel.cpp:91-191,
  * kernels/flash_attention_mx_gemma/kernel.cpp:124-213).  Needs no workspace: every workgroup
- * widens the K blocks it reads to bf16 in LDS (exact), and an E3M2 V tile is read by the PV
- * MFMA as E5M2 (the same bits, sign moved; O rescaled by 2^12, exact).  Three 4-wave
+ * widens the K blocks it reads to bf16 in LDS (exact), an E3M2 V tile is read by the PV
+ * MFMA as E5M2 (the same bits, sign moved; O rescaled by 2^12, exact) and a block-packed
+ * E3M2 V tile (MXFA_FMT_E3M2_BLK) as the MFMA's fp6 operand, as it is.  Three 4-wave
  * workgroups per CU for head_dim <= 128, two for 256. */
 mxfa_status mxfa_prefill(const mxfa_attn_params *p,
                          const uint8_t *q, const uint8_t *q_sc,
@@ -128,8 +139,9 @@ mxfa_status mxfa_prefill(const mxfa_attn_params *p,
  * (about 16 * wave-blocks < 32 * batch * num_kv_heads * seq_k, e.g. one query head per KV
  * head), the call runs mxfa_prefill's kernel instead and leaves the workspace untouched.  Same
  * inputs, outputs and O as mxfa_prefill (bit-identical with E4M3 V, where both run the same
- * arithmetic in the same order; within a few ulps with E3M2 V).
- * *workspace_bytes = batch * num_kv_heads * seq_k * head_dim * (2, or 3 with E3M2 V).  A
+ * arithmetic in the same order; within a few ulps with E3M2 V).  Block-packed E3M2 V needs no
+ * copy: the kernel reads it from v as it is.
+ * *workspace_bytes = batch * num_kv_heads * seq_k * head_dim * (2, or 3 with MXFA_FMT_E3M2 V).  A
  * workspace smaller than the plan is MXFA_ERR_WORKSPACE.
  * Replaces the same reference entry point as mxfa_prefill (kernels/flash_attention_mx_gqa/
  * kernel.cpp:91-191); the reference's matrix unit takes K's codes and scales as they are, so
@@ -142,7 +154,7 @@ mxfa_status mxfa_prefill_ws(const mxfa_attn_params *p,
                             const uint8_t *v, const uint8_t *v_sc,
                             float *o, void *workspace, size_t workspace_bytes, void *stream);
 
-/* Test entry: the stages of the workspace prefill for query rows 32 * q_tile .. + 31 of head bh
+/* Test entry (V as E4M3 or E3M2 codes): the stages of the workspace prefill for query rows 32 * q_tile .. + 31 of head bh
  * (= batch * num_q_heads + query head), as its own routines compute them.  Runs the one
  * workgroup of mxfa_prefill_ws that holds those rows (writing their O rows, bit-identical to
  * mxfa_prefill_ws) and records, for each key block the workgroup processes:
@@ -193,7 +205,9 @@ mxfa_status mxfa_decode_noalloc(const mxfa_attn_params *p,
 /* ---- KV cache ---- */
 
 /* KV-cache shape for mxfa_kv_append: caches k [B][Hkv][max_len][D] + k_sc [B][Hkv][max_len][D/32],
- * v [B][Hkv][max_len][D] + v_sc [B][Hkv][max_len/32][D] (the layouts mxfa_decode reads). */
+ * v [B][Hkv][max_len][D] + v_sc [B][Hkv][max_len/32][D] (the layouts mxfa_decode reads); with
+ * v_fmt MXFA_FMT_E3M2_BLK, v [B][Hkv][max_len/32][D][24] (read by the prefill entry points
+ * only; mxfa_decode returns MXFA_ERR_UNSUPPORTED for it). */
 typedef struct {
   int32_t batch, num_kv_heads;
   int32_t head_dim;                         /* multiple of 32                                 */

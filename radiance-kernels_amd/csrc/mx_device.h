@@ -165,6 +165,21 @@ __device__ __forceinline__ uint32_t e3m2_code_bf16(uint32_t h) {
   return (neg << 5) | c;
 }
 
+// Element i (a 6-bit code) of a 32-element block packed little endian into six dwords: bits
+// 6i .. 6i + 5 of the 192 (i a compile-time constant after unrolling).
+// Field of row r (0..31) in a block-packed E3M2 block: rows 8g + 4a + b (g < 4, a < 2, b < 4)
+// at field 16a + 4g + b.  The attention kernels' P operand holds, in lane half a, byte 4g +
+// b of each 16-byte half t, the probability of key 32t + 8g + 4a + b; the scaled MFMA pairs
+// that byte with fp6 A field 16a + 4g + b of lane half t, so V stored in this order is read
+// with the key order P has.
+__device__ __forceinline__ constexpr int blk6_field(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
+
+__device__ __forceinline__ void pack6(uint32_t (&w)[6], int i, uint32_t code) {
+  const int bit = 6 * i;
+  w[bit / 32] |= code << (bit % 32);
+  if (bit % 32 > 26) w[bit / 32 + 1] |= code >> (32 - bit % 32);
+}
+
 // E3M2 codes (low 6 bits of each byte) -> E4M3 codes of the same values (exact:
 // every E3M2 value is an E4M3 value), four per dword.
 __device__ __forceinline__ uint32_t e3m2x4_to_e4m3x4(uint32_t w) {

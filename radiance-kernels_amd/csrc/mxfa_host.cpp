@@ -64,6 +64,12 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3n_d64_softcap_e3m2", "mxfa_prefill3n_d128_softcap_e3m2", "mxfa_prefill3n_d256_softcap_e3m2",
     "mxfa_prefill3n_d64_r2_e3m2", "mxfa_prefill3n_d128_r2_e3m2", "mxfa_prefill3n_d256_r2_e3m2",
     "mxfa_prefill3n_d64_softcap_r2_e3m2", "mxfa_prefill3n_d128_softcap_r2_e3m2", "mxfa_prefill3n_d256_softcap_r2_e3m2",
+    "mxfa_quant_cols_e3m2_blk", "mxfa_kv_append_e3m2_blk",
+#define MXFA_BLK_NAMES(D)                                                                                      \
+  "mxfa_prefill3_d" #D "_blk", "mxfa_prefill3_d" #D "_softcap_blk", "mxfa_prefill3_d" #D "_r2_blk",            \
+      "mxfa_prefill3_d" #D "_softcap_r2_blk", "mxfa_prefill3n_d" #D "_blk", "mxfa_prefill3n_d" #D "_softcap_blk", \
+      "mxfa_prefill3n_d" #D "_r2_blk", "mxfa_prefill3n_d" #D "_softcap_r2_blk"
+    MXFA_BLK_NAMES(64), MXFA_BLK_NAMES(128), MXFA_BLK_NAMES(256),
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -173,13 +179,15 @@ mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
   if (!(p->softmax_scale > 0.0f) || !std::isfinite(p->softmax_scale))
     return fail(MXFA_ERR_INVALID_ARG, "softmax_scale must be finite and > 0");
   if (!(p->softcap >= 0.0f) || !std::isfinite(p->softcap)) return fail(MXFA_ERR_INVALID_ARG, "softcap must be finite and >= 0");
-  if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "v_fmt must be E4M3 or E3M2");
+  if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2 && p->v_fmt != MXFA_FMT_E3M2_BLK)
+    return fail(MXFA_ERR_INVALID_ARG, "v_fmt must be E4M3, E3M2 or E3M2_BLK");
   if (p->block_n != 0 && p->block_n != 64) return fail(MXFA_ERR_UNSUPPORTED, "block_n must be 0 (default) or 64");
   if (p->p_rule != MXFA_P_R1 && p->p_rule != MXFA_P_R2) return fail(MXFA_ERR_INVALID_ARG, "p_rule must be R1 or R2");
   if (p->kv_stride != 0 && (p->kv_stride < p->seq_k || p->kv_stride % 32))
     return fail(MXFA_ERR_INVALID_ARG, "kv_stride must be 0 or a multiple of 32 that is >= seq_k");
   if (decode) {
     if (p->seq_q != 1) return fail(MXFA_ERR_INVALID_ARG, "decode needs seq_q == 1");
+    if (p->v_fmt == MXFA_FMT_E3M2_BLK) return fail(MXFA_ERR_UNSUPPORTED, "decode reads V as E4M3 or E3M2 codes, not E3M2_BLK");
     if (p->num_q_heads / p->num_kv_heads > 32)
       return fail(MXFA_ERR_UNSUPPORTED, "decode supports at most 32 query heads per KV head");
   }
@@ -220,10 +228,13 @@ FaArgs make_args(const mxfa_attn_params* p, const uint8_t* q, const uint8_t* qs,
   return a;
 }
 
-const char* kernel_name(const char* kind, const mxfa_attn_params* p, bool e3m2_suffix = false) {
+// Kernel name for a parameter set; v_suffix adds the V-format suffix of the prefill kernels
+// ("_e3m2": E3M2 codes rewritten in LDS, "_blk": block-packed E3M2 read as fp6).
+const char* kernel_name(const char* kind, const mxfa_attn_params* p, bool v_suffix = false) {
   static thread_local char buf[64];
+  const char* vs = !v_suffix ? "" : p->v_fmt == MXFA_FMT_E3M2 ? "_e3m2" : p->v_fmt == MXFA_FMT_E3M2_BLK ? "_blk" : "";
   std::snprintf(buf, sizeof buf, "mxfa_%s_d%d%s%s%s", kind, p->head_dim, p->softcap > 0.0f ? "_softcap" : "",
-                p->p_rule == MXFA_P_R2 ? "_r2" : "", e3m2_suffix ? "_e3m2" : "");
+                p->p_rule == MXFA_P_R2 ? "_r2" : "", vs);
   return buf;
 }
 
@@ -320,7 +331,7 @@ mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32
                                uint8_t* scales, void* stream) {
   if (mats < 0 || rows <= 0 || rows % 32 || cols <= 0 || cols % 4)
     return fail(MXFA_ERR_INVALID_ARG, "rows must be a positive multiple of 32 and cols of 4");
-  if (fmt != MXFA_FMT_E4M3 && fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad fmt");
+  if (fmt != MXFA_FMT_E4M3 && fmt != MXFA_FMT_E3M2 && fmt != MXFA_FMT_E3M2_BLK) return fail(MXFA_ERR_INVALID_ARG, "bad fmt");
   if (mats == 0) return MXFA_OK;
   if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u) || (reinterpret_cast<uintptr_t>(scales) & 3u))
@@ -330,7 +341,9 @@ mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32
   int64_t threads = mats * (rows / 32) * (cols / 4);
   dim3 grid((unsigned)((threads + 255) / 256));
   void* args[] = {(void*)&x, &mats, &rows, &cols, &codes, &scales};
-  return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : "mxfa_quant_cols_e3m2", grid, dim3(256), args, stream);
+  return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : fmt == MXFA_FMT_E3M2 ? "mxfa_quant_cols_e3m2"
+                                                                                        : "mxfa_quant_cols_e3m2_blk",
+                grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_kv_append(const mxfa_kv_params* p, const float* k_new, const float* v_new, int32_t pos0, int32_t n_new,
@@ -340,7 +353,8 @@ mxfa_status mxfa_kv_append(const mxfa_kv_params* p, const float* k_new, const fl
   if (p->batch < 1 || p->num_kv_heads < 1) return fail(MXFA_ERR_INVALID_ARG, "batch and num_kv_heads must be >= 1");
   if (p->head_dim < 32 || p->head_dim % 32) return fail(MXFA_ERR_INVALID_ARG, "head_dim must be a positive multiple of 32");
   if (p->max_len < 32 || p->max_len % 32) return fail(MXFA_ERR_INVALID_ARG, "max_len must be a positive multiple of 32");
-  if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2) return fail(MXFA_ERR_INVALID_ARG, "bad v_fmt");
+  if (p->v_fmt != MXFA_FMT_E4M3 && p->v_fmt != MXFA_FMT_E3M2 && p->v_fmt != MXFA_FMT_E3M2_BLK)
+    return fail(MXFA_ERR_INVALID_ARG, "bad v_fmt");
   if (pos0 < 0 || n_new < 0 || (int64_t)pos0 + n_new > p->max_len)
     return fail(MXFA_ERR_INVALID_ARG, "need 0 <= pos0 and pos0 + n_new <= max_len");
   if (n_new == 0) return MXFA_OK;
@@ -364,7 +378,9 @@ mxfa_status mxfa_kv_append(const mxfa_kv_params* p, const float* k_new, const fl
   if (kgroups + vgroups > 0x7fffffffLL) return fail(MXFA_ERR_UNSUPPORTED, "append too large for one launch");
   void* args[] = {(void*)&k_new, (void*)&v_new, &v_tail, &kblocks, &kgroups, &vunits, &ntouch,
                   &n, &L, &D, &pos, &k_cache, &k_sc, &v_cache, &v_sc};
-  if (mxfa_status st = launch(dm, p->v_fmt == MXFA_FMT_E4M3 ? "mxfa_kv_append_e4m3" : "mxfa_kv_append_e3m2",
+  if (mxfa_status st = launch(dm, p->v_fmt == MXFA_FMT_E4M3   ? "mxfa_kv_append_e4m3"
+                                  : p->v_fmt == MXFA_FMT_E3M2 ? "mxfa_kv_append_e3m2"
+                                                              : "mxfa_kv_append_e3m2_blk",
                               dim3((unsigned)(kgroups + vgroups)), dim3(256), args, stream))
     return st;
   if (end % 32 == 0 || ntouch == 1) return MXFA_OK;   // no open block, or its tail is already written
@@ -520,7 +536,7 @@ mxfa_status mxfa_prefill(const mxfa_attn_params* p, const uint8_t* q, const uint
   void* args[] = {&a};
   // the workspace kernel's design in its workspace-free form: K widened to bf16 in LDS, E3M2
   // V read as E5M2
-  return launch(dm, kernel_name("prefill3n", p, p->v_fmt == MXFA_FMT_E3M2), grid, dim3(256), args, stream);
+  return launch(dm, kernel_name("prefill3n", p, true), grid, dim3(256), args, stream);
 }
 
 mxfa_status mxfa_prefill_plan(const mxfa_attn_params* p, size_t* workspace_bytes) {
@@ -557,9 +573,11 @@ mxfa_status prefill_ws_impl(const mxfa_attn_params* p, const uint8_t* q, const u
   FaArgs a = prefill_args(p, q, q_sc, k, k_sc, v, v_sc, o, nw, grid);
   if (!tr && prefill_ws_widens_in_lds(a, p)) {
     void* args[] = {&a};
-    return launch(dm, kernel_name("prefill3n", p, p->v_fmt == MXFA_FMT_E3M2), grid, dim3(256), args, stream);
+    return launch(dm, kernel_name("prefill3n", p, true), grid, dim3(256), args, stream);
   }
   uint8_t* kbf = static_cast<uint8_t*>(workspace);
+  // (E3M2 V codes one per byte: widened to E4M3 by the pre-pass; block-packed E3M2 V is read
+  // by the kernel as it is)
   uint8_t* vws = p->v_fmt == MXFA_FMT_E3M2 ? kbf + prefill3_kbf_bytes(p) : nullptr;
   a.kbf = kbf;
   a.vws = vws;
@@ -572,7 +590,8 @@ mxfa_status prefill_ws_impl(const mxfa_attn_params* p, const uint8_t* q, const u
   void* cargs[] = {(void*)&k, (void*)&k_sc, (void*)&v, &D, &Sk, &Skc, &kbf, &vws};
   if (mxfa_status st = launch(dm, "mxfa_k_to_bf16", cgrid, dim3(256), cargs, stream)) return st;
   void* args[] = {&a};
-  if (!tr) return launch(dm, kernel_name("prefill3", p), grid, dim3((unsigned)(64 * nw)), args, stream);
+  if (!tr) return launch(dm, kernel_name("prefill3", p, p->v_fmt == MXFA_FMT_E3M2_BLK), grid, dim3((unsigned)(64 * nw)),
+                         args, stream);
   // the item (qx, qy) of the traced rows, as the kernel's own mapping assigns them
   const int b = tr->bh / p->num_q_heads, head = tr->bh % p->num_q_heads;
   const int kvh = head / a.group, hc = (head % a.group) / a.hpw;
@@ -606,6 +625,7 @@ mxfa_status mxfa_prefill_trace(const mxfa_attn_params* p, const uint8_t* q, cons
   if (bh < 0 || bh >= p->batch * p->num_q_heads || q_tile < 0 || 32 * q_tile >= p->seq_q)
     return fail(MXFA_ERR_INVALID_ARG, "bh or q_tile out of range");
   if (!s_out || !ml_out || !p_out || !ps_out) return fail(MXFA_ERR_INVALID_ARG, "NULL trace buffer");
+  if (p->v_fmt == MXFA_FMT_E3M2_BLK) return fail(MXFA_ERR_UNSUPPORTED, "the stage trace reads V as E4M3 or E3M2 codes");
   const TraceReq tr = {bh, q_tile, s_out, ml_out, p_out, ps_out};
   return prefill_ws_impl(p, q, q_sc, k, k_sc, v, v_sc, o, workspace, workspace_bytes, stream, &tr);
 }

@@ -117,6 +117,10 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_r4(const float
 
 // 32-blocks along rows (V layout): each lane owns 4 adjacent columns of one
 // 32-row block.  mats matrices of rows x cols; rows % 32 == 0, cols % 4 == 0.
+// FMT 2: E3M2, each 32-row block of a column stored as 24 bytes at codes + ((m * rows / 32 +
+// rb) * cols + c) * 24, row r's code in field blk6_field(r) (bits 6f .. 6f + 5, little
+// endian): the fp6 A operand of the scaled MFMA in the key order of the P operand the
+// attention kernels build.
 template <int FMT>
 __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int rows, int cols,
                                 uint8_t* __restrict__ codes, uint8_t* __restrict__ scales) {
@@ -137,13 +141,34 @@ __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int r
   const int lp = FMT == 0 ? 8 : 4;
   uint32_t s0 = scale_code(amax.x, lp), s1 = scale_code(amax.y, lp), s2 = scale_code(amax.z, lp),
            s3 = scale_code(amax.w, lp);
+  if constexpr (FMT == 2) {
+    uint32_t pk[4][6] = {};
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
+      const uint32_t c[4] = {e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.x, 127 - (int)s0))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.y, 127 - (int)s1))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.z, 127 - (int)s2))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.w, 127 - (int)s3)))};
+#pragma unroll
+      for (int q = 0; q < 4; q++) pack6(pk[q], blk6_field(r), c[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(codes + ((m * (rows / 32) + rb) * cols + c4 + q) * 24);
+#pragma unroll
+      for (int w = 0; w < 6; w++) dst[w] = pk[q][w];
+    }
+    *reinterpret_cast<uint32_t*>(scales + (m * (rows / 32) + rb) * cols + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
+    return;
+  }
   uint8_t* cbase = codes + (m * rows + (int64_t)rb * 32) * cols + c4;
   for (int r = 0; r < 32; r++) {
     float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
     float y0 = __builtin_ldexpf(v.x, 127 - (int)s0), y1 = __builtin_ldexpf(v.y, 127 - (int)s1);
     float y2 = __builtin_ldexpf(v.z, 127 - (int)s2), y3 = __builtin_ldexpf(v.w, 127 - (int)s3);
     uint32_t w;
-    if (FMT == 0)
+    if constexpr (FMT == 0)
       w = e4m3_code4(y0, y1, y2, y3);
     else
       w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
@@ -160,6 +185,10 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e4m3(const flo
 extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e3m2(const float* x, int64_t mats, int rows, int cols,
                                                                        uint8_t* codes, uint8_t* scales) {
   quant_cols_impl<1>(x, mats, rows, cols, codes, scales);
+}
+extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e3m2_blk(const float* x, int64_t mats, int rows,
+                                                                           int cols, uint8_t* codes, uint8_t* scales) {
+  quant_cols_impl<2>(x, mats, rows, cols, codes, scales);
 }
 
 // ============================================================================
@@ -235,13 +264,38 @@ __device__ __forceinline__ void kv_append_v_part(const float* v_new, float* v_ta
   const uint32_t s0 = scale_code(amax.x, lp), s1 = scale_code(amax.y, lp), s2 = scale_code(amax.z, lp),
                  s3 = scale_code(amax.w, lp);
   const bool tail_here = ntouch == 1 && (end % 32) != 0;
+  if constexpr (FMT == 2) {
+    // rows 4 rl .. 4 rl + 3 of a column are the consecutive fields blk6_field(4 rl) .. + 3 of
+    // its 24-byte block: three bytes per column at byte 12 (rl % 2) + 3 (rl / 2)
+    uint32_t pk[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c[4] = {e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].x, 127 - (int)s0))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].y, 127 - (int)s1))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].z, 127 - (int)s2))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].w, 127 - (int)s3)))};
+#pragma unroll
+      for (int q = 0; q < 4; q++) pk[q] |= c[q] << (6 * i);
+      if (tail_here && p0 + 4 * rl + i >= pos0) *reinterpret_cast<float4*>(v_tail + (bk * 32 + 4 * rl + i) * D + c4) = x[i];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint8_t* dst = v_cache + ((bk * (L / 32) + blk) * D + c4 + q) * 24 + 12 * (rl & 1) + 3 * (rl >> 1);
+      dst[0] = (uint8_t)pk[q];
+      dst[1] = (uint8_t)(pk[q] >> 8);
+      dst[2] = (uint8_t)(pk[q] >> 16);
+    }
+    if (rl == 0)
+      *reinterpret_cast<uint32_t*>(v_sc + (bk * (L / 32) + blk) * D + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = 4 * rl + i;
     const float y0 = __builtin_ldexpf(x[i].x, 127 - (int)s0), y1 = __builtin_ldexpf(x[i].y, 127 - (int)s1);
     const float y2 = __builtin_ldexpf(x[i].z, 127 - (int)s2), y3 = __builtin_ldexpf(x[i].w, 127 - (int)s3);
     uint32_t w;
-    if (FMT == 0)
+    if constexpr (FMT == 0)
       w = e4m3_code4(y0, y1, y2, y3);
     else
       w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
@@ -276,6 +330,7 @@ __device__ void kv_append_impl(const float* k_new, const float* v_new, float* v_
   }
 MXFA_KV_APPEND(0, mxfa_kv_append_e4m3)
 MXFA_KV_APPEND(1, mxfa_kv_append_e3m2)
+MXFA_KV_APPEND(2, mxfa_kv_append_e3m2_blk)
 
 // Tail of the block left open by an append that spans several blocks: rows of positions
 // pos0 .. end - 1 from the new tokens, rows past the end zeroed (the block starts after
@@ -350,6 +405,11 @@ __device__ __forceinline__ v16f mfma_mx(v8i a, v8i b, v16f c, int sa, int sb) {
 // A operand in E5M2 (cbsz = 1), B in E4M3
 __device__ __forceinline__ v16f mfma_mx_a5(v8i a, v8i b, v16f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 0, 0, sa, 0, sb);
+}
+// A operand in fp6 E3M2 (cbsz = 3: lane l holds row l % 32 and k = 32 (l / 32) + i, element i
+// in bits 6i .. 6i + 5 of dwords 0-5, measured on gfx950), B in E4M3
+__device__ __forceinline__ v16f mfma_mx_a6(v8i a, v8i b, v16f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 3, 0, 0, sa, 0, sb);
 }
 
 __device__ __forceinline__ v16f mfma_bf16(v4i a, v4i b, v16f c) {
@@ -935,6 +995,36 @@ __device__ __forceinline__ void pv_parts(v16f (&o)[D / 32], const uint8_t* sv, c
   }
 }
 
+// PV of one block with V in the E3M2 block-packed layout: the LDS tile holds, per 32-key block
+// kb (0, 1) and d, the block's 24 bytes at kb * 24D + 24 d -- exactly the fp6 A operand of
+// lane (d % 32) + 32 kb, read with three ds_read_b64 (lanes 24 bytes apart: 32 distinct
+// even banks, conflict-free).  V scales follow at BN * D as for E4M3 V.
+template <int D, int NP>
+__device__ __forceinline__ void pv_parts_blk(v16f (&o)[D / 32], const uint8_t* sv, const v8i& pb,
+                                             const int (&psc)[BN / 32], int lane) {
+  constexpr int NT = D / 32 / NP;
+  const int r = lane & 31, h = lane >> 5;
+  const int hmask = -(int)__builtin_amdgcn_ubfe((uint32_t)lane, 5, 1);
+  const int pscale = psc[0] ^ ((psc[0] ^ psc[1]) & hmask);
+  const uint8_t* a0 = sv + h * (24 * D) + 24 * r;
+#pragma unroll
+  for (int part = 0; part < NP; part++) {
+    v8i va[NT];
+    int vs[NT];
+#pragma unroll
+    for (int u = 0; u < NT; u++) {
+      const int dt = part * NT + u;
+      const v2i* src = reinterpret_cast<const v2i*>(a0 + 768 * dt);
+      const v2i x0 = src[0], x1 = src[1], x2 = src[2];
+      va[u] = (v8i){x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], 0, 0};
+      vs[u] = sv[BN * D + h * D + dt * 32 + r];
+    }
+#pragma unroll
+    for (int u = 0; u < NT; u++) o[part * NT + u] = mfma_mx_a6(va[u], pb, o[part * NT + u], vs[u], pscale);
+    if (part + 1 < NP) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // O of one wave (32 query rows x D, MFMA layout), normalized by inv, stored through LDS so
 // that every store instruction writes whole 128-byte lines: a lane of the MFMA layout holds
 // 16-byte pieces of its row 128 bytes apart, whose line-partial stores cost 20% extra HBM
@@ -1095,8 +1185,22 @@ __device__ __forceinline__ P3Src p3_src(const uint8_t* kbf, const uint8_t* v, co
   return {buf_rsrc(kbf, 0, (int64_t)Sk * (2 * D)), buf_rsrc(v, 0, (int64_t)Sk * D), buf_rsrc(vs, 0, (int64_t)(Sk / 32) * D)};
 }
 
-template <int D, int NW, bool DO_K = true, bool DO_V = true>
-__device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v, int key0, int wave, const P3Lane& pl) {
+// V of block-packed E3M2 (VBLK): the block's two 32-key MX blocks are 48 D contiguous bytes
+// of the caller's array (24 per (32-key block, d)), copied as they are by 3D / 64 one-KB
+// instructions dealt to the waves in turn.
+template <int D, int NW>
+__device__ __forceinline__ void p3_dma_vblk(__amdgpu_buffer_rsrc_t rv, uint8_t* v, int key0, int wave, int lane) {
+  constexpr int NV = 48 * D / 1024;
+#pragma unroll
+  for (int m = 0; m < (NV + NW - 1) / NW; m++) {
+    const int i = wave + NW * m;
+    if (NV % NW == 0 || i < NV) dma_lds<16>(rv, v + i * 1024, lane * 16, (key0 / 32) * (24 * D) + i * 1024);
+  }
+}
+
+template <int D, int NW, bool DO_K = true, bool DO_V = true, bool VBLK = false>
+__device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v, int key0, int wave, const P3Lane& pl,
+                                       int lane = 0) {
   using L = P3Lds<D>;
   constexpr int WPG = NW / 4, IPW = 2 * D / 64 / WPG;   // waves per 16-row group, K instructions per wave
   constexpr int VPW = L::VDMA / NW;                     // V instructions per wave
@@ -1105,13 +1209,16 @@ __device__ __forceinline__ void p3_dma(const P3Src& src, uint8_t* kb, uint8_t* v
 #pragma unroll
     for (int m = 0; m < IPW; m++) dma_lds<16>(src.k, kdst + m * 1024, pl.k, key0 * (2 * D) + 64 * m);
   }
-  if constexpr (DO_V) {
+  if constexpr (DO_V && VBLK) p3_dma_vblk<D, NW>(src.v, v, key0, wave, lane);
+  if constexpr (DO_V && !VBLK) {
     const int i0 = p3_v_instr<D, NW>(wave, 0);
 #pragma unroll
     for (int m = 0; m < VPW; m++) {
       const int i = p3_v_instr<D, NW>(wave, m);
       dma_lds<16>(src.v, v + i * 1024, pl.v, key0 * D + (i - i0) * 1024);
     }
+  }
+  if constexpr (DO_V) {
 #pragma unroll
     for (int m = 0; m < (2 * D + 255) / 256; m++) dma_lds<4>(src.vs, v + L::V + m * 256, pl.s, (key0 / 32) * D + m * 256);
   }
@@ -1157,7 +1264,7 @@ struct P3NSrc {
   __amdgpu_buffer_rsrc_t k8, ks, v, vs;
 };
 
-template <int D>
+template <int D, bool VBLK = false>
 __device__ __forceinline__ void p3n_dma(const P3NSrc& src, uint8_t* kb, uint8_t* ksc, uint8_t* v, int key0, int wave,
                                         int lane, const P3Lane& pl) {
   using L = P3Lds<D>;
@@ -1170,12 +1277,16 @@ __device__ __forceinline__ void p3n_dma(const P3NSrc& src, uint8_t* kb, uint8_t*
   // K scales: BN * D / 32 bytes, 256 per dword instruction, from waves 0 (and 1 at D = 256)
   if (wave < (BN * D / 32 + 255) / 256) dma_lds<4>(src.ks, ksc + wave * 256, lane * 4, key0 * (D / 32) + wave * 256);
   // V codes and scales as the workspace form
-  constexpr int VPW = L::VDMA / 4;
-  const int i0 = p3_v_instr<D, 4>(wave, 0);
+  if constexpr (VBLK) {
+    p3_dma_vblk<D, 4>(src.v, v, key0, wave, lane);
+  } else {
+    constexpr int VPW = L::VDMA / 4;
+    const int i0 = p3_v_instr<D, 4>(wave, 0);
 #pragma unroll
-  for (int m = 0; m < VPW; m++) {
-    const int i = p3_v_instr<D, 4>(wave, m);
-    dma_lds<16>(src.v, v + i * 1024, pl.v, key0 * D + (i - i0) * 1024);
+    for (int m = 0; m < VPW; m++) {
+      const int i = p3_v_instr<D, 4>(wave, m);
+      dma_lds<16>(src.v, v + i * 1024, pl.v, key0 * D + (i - i0) * 1024);
+    }
   }
 #pragma unroll
   for (int m = 0; m < (2 * D + 255) / 256; m++) dma_lds<4>(src.vs, v + L::V + m * 256, pl.s, (key0 / 32) * D + m * 256);
@@ -1233,7 +1344,9 @@ __device__ __forceinline__ int fresh_lane() {
 // NOWS: the workspace-free form (mxfa_prefill): K read as E4M3 codes and widened to bf16 in
 // LDS by p3n_widen_k at the top of every block (one K stage), V read from the caller's array;
 // VE3: V is E3M2, rewritten in LDS as E5M2 (p3n_v_e3m2_to_e5m2), O scaled by 2^12.
-template <int D, bool SOFTCAP, int PR, bool TRACE = false, bool NOWS = false, bool VE3 = false>
+// VBLK: V is E3M2 in the block-packed layout ([Skc / 32][D][24 bytes] per (b, KV head)),
+// copied into LDS as it is and read by the PV MFMA as its fp6 operand (pv_parts_blk).
+template <int D, bool SOFTCAP, int PR, bool TRACE = false, bool NOWS = false, bool VE3 = false, bool VBLK = false>
 __device__ void prefill3_impl(const FaArgs& a) {
   using L = P3Lds<D>;
   constexpr int NW = P3Waves<D>::N;
@@ -1282,15 +1395,20 @@ __device__ void prefill3_impl(const FaArgs& a) {
   const bool wave_live = qw0 < a.Sq;
 
   // V codes: the caller's E4M3 V, or its E4M3 copy (dense, Sk keys) when V is E3M2
-  const P3Src src = NOWS ? P3Src{} : p3_src(a.kbf + (int64_t)bk * a.Sk * (2 * D),
-                                           a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
-                                           a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk, D);
+  const P3Src src = NOWS   ? P3Src{}
+                    : VBLK ? P3Src{buf_rsrc(a.kbf, (int64_t)bk * a.Sk * (2 * D), (int64_t)a.Sk * (2 * D)),
+                                   buf_rsrc(a.v, (int64_t)bk * (a.Skc / 32) * (24 * D), (int64_t)(a.Sk / 32) * (24 * D)),
+                                   buf_rsrc(a.vs, (int64_t)bk * (a.Skc / 32) * D, (int64_t)(a.Sk / 32) * D)}
+                           : p3_src(a.kbf + (int64_t)bk * a.Sk * (2 * D),
+                                    a.vws ? a.vws + (int64_t)bk * a.Sk * D : a.v + (int64_t)bk * a.Skc * D,
+                                    a.vs + (int64_t)bk * (a.Skc / 32) * D, a.Sk, D);
   // workspace-free: the caller's K codes and scales, V and V scales (Skc keys apart), each
   // resource ending at key Sk
   const P3NSrc nsrc = !NOWS ? P3NSrc{}
                             : P3NSrc{buf_rsrc(a.k, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D),
                                      buf_rsrc(a.ks, (int64_t)bk * a.Skc * (D / 32), (int64_t)a.Sk * (D / 32)),
-                                     buf_rsrc(a.v, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D),
+                                     VBLK ? buf_rsrc(a.v, (int64_t)bk * (a.Skc / 32) * (24 * D), (int64_t)(a.Sk / 32) * (24 * D))
+                                          : buf_rsrc(a.v, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D),
                                      buf_rsrc(a.vs, (int64_t)bk * (a.Skc / 32) * D, (int64_t)(a.Sk / 32) * D)};
   const P3Lane pl = p3_lane<D, NW>(wave, lane);
   // loop-invariant operands in VGPRs at three waves per SIMD (D <= 128), in SGPRs at two (D =
@@ -1311,8 +1429,8 @@ __device__ void prefill3_impl(const FaArgs& a) {
   };
 
   if (j0 < j1) {
-    if constexpr (NOWS) p3n_dma<D>(nsrc, sKb0, sKs, sV0, j0 * BN, wave, lane, pl);
-    else p3_dma<D, NW>(src, sKb0, sV0, j0 * BN, wave, pl);
+    if constexpr (NOWS) p3n_dma<D, VBLK>(nsrc, sKb0, sKs, sV0, j0 * BN, wave, lane, pl);
+    else p3_dma<D, NW, true, true, VBLK>(src, sKb0, sV0, j0 * BN, wave, pl, lane);
   }
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
   __syncthreads();
@@ -1347,10 +1465,10 @@ __device__ void prefill3_impl(const FaArgs& a) {
     if constexpr (K1) {
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's K operand reads are done
       __builtin_amdgcn_s_barrier();
-      if constexpr (NOWS) p3n_dma<D>(nsrc, kb_dma, sKs, v_dma, (j + 1) * BN, wave, fresh_lane(), pl);
-      else p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+      if constexpr (NOWS) p3n_dma<D, VBLK>(nsrc, kb_dma, sKs, v_dma, (j + 1) * BN, wave, fresh_lane(), pl);
+      else p3_dma<D, NW, true, true, VBLK>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl, fresh_lane());
     } else {
-      p3_dma<D, NW>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl);
+      p3_dma<D, NW, true, true, VBLK>(src, kb_dma, v_dma, (j + 1) * BN, wave, pl, lane);
       p3_dma_interleave<D>();
     }
     if constexpr (D <= 128) __builtin_amdgcn_s_setprio(0);
@@ -1403,7 +1521,8 @@ __device__ void prefill3_impl(const FaArgs& a) {
         for (int i = 0; i < 16; i++) o[dt][i] *= corr;
     }
     // D <= 128: the PV addresses stay in registers (loop-invariant); D = 256 has no room
-    pv_parts<D, D == 256 ? 2 : 1, VE3>(o, v_cur, pb, psc, D == 256 ? fresh_lane() : lane);
+    if constexpr (VBLK) pv_parts_blk<D, D == 256 ? 2 : 1>(o, v_cur, pb, psc, D == 256 ? fresh_lane() : lane);
+    else pv_parts<D, D == 256 ? 2 : 1, VE3>(o, v_cur, pb, psc, D == 256 ? fresh_lane() : lane);
     __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);   // vmcnt(0) lgkmcnt(0): next stage landed
     __builtin_amdgcn_s_barrier();
   };
@@ -1453,6 +1572,23 @@ MXFA_PREFILL3(256, false, P_R1, mxfa_prefill3_d256)
 MXFA_PREFILL3(256, true, P_R1, mxfa_prefill3_d256_softcap)
 MXFA_PREFILL3(256, false, P_R2, mxfa_prefill3_d256_r2)
 MXFA_PREFILL3(256, true, P_R2, mxfa_prefill3_d256_softcap_r2)
+// E3M2 V in the block-packed layout (the pre-pass widens K only)
+#define MXFA_PREFILL3B(D, SC, PR, NOWS, NAME)                                                        \
+  extern "C" __global__ void __launch_bounds__(256, D == 256 ? 2 : 3) NAME(FaArgs a) {               \
+    prefill3_impl<D, SC, PR, false, NOWS, false, true>(a);                                           \
+  }
+#define MXFA_PREFILL3B_ALL(D)                                                                        \
+  MXFA_PREFILL3B(D, false, P_R1, false, mxfa_prefill3_d##D##_blk)                                    \
+  MXFA_PREFILL3B(D, true, P_R1, false, mxfa_prefill3_d##D##_softcap_blk)                             \
+  MXFA_PREFILL3B(D, false, P_R2, false, mxfa_prefill3_d##D##_r2_blk)                                 \
+  MXFA_PREFILL3B(D, true, P_R2, false, mxfa_prefill3_d##D##_softcap_r2_blk)                          \
+  MXFA_PREFILL3B(D, false, P_R1, true, mxfa_prefill3n_d##D##_blk)                                    \
+  MXFA_PREFILL3B(D, true, P_R1, true, mxfa_prefill3n_d##D##_softcap_blk)                             \
+  MXFA_PREFILL3B(D, false, P_R2, true, mxfa_prefill3n_d##D##_r2_blk)                                 \
+  MXFA_PREFILL3B(D, true, P_R2, true, mxfa_prefill3n_d##D##_softcap_r2_blk)
+MXFA_PREFILL3B_ALL(64)
+MXFA_PREFILL3B_ALL(128)
+MXFA_PREFILL3B_ALL(256)
 
 // Workspace-free prefill (mxfa_prefill, and mxfa_prefill_ws where widening K per workgroup
 // costs less than the pre-pass): K widened in LDS, E3M2 V read as E5M2.

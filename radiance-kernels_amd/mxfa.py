@@ -28,6 +28,7 @@ LIB_PATH = os.path.join(HERE, "libmxfa.so")
 
 FMT_E4M3 = 0
 FMT_E3M2 = 1
+FMT_E3M2_BLK = 2    # E3M2 V packed per 32-row MX block: [..., rows/32, cols, 24] bytes (the MFMA fp6 operand)
 P_R1 = 0        # P requant rule of lib/golden (default)
 P_R2 = 1        # the reference device kernels' truncating "target-0" rule
 DEFAULT_BLOCK_N = 64
@@ -83,7 +84,7 @@ def _check_attn_operands(p, q, qs, k, ks, v, vs, out):
     _need(qs, u8, (B, Hq, Sq, D // 32), "q_sc")
     _need(k, u8, (B, Hkv, L, D), "k")
     _need(ks, u8, (B, Hkv, L, D // 32), "k_sc")
-    _need(v, u8, (B, Hkv, L, D), "v")
+    _need(v, u8, (B, Hkv, L // 32, D, 24) if p.v_fmt == FMT_E3M2_BLK else (B, Hkv, L, D), "v")
     _need(vs, u8, (B, Hkv, L // 32, D), "v_sc")
     _need(out, torch.float32, (B, Hq, Sq, D), "out")
 
@@ -192,15 +193,56 @@ def quantize_rows_r4(x, stream=None):
 
 def quantize_cols(x, fmt=FMT_E4M3, stream=None):
     """x: contiguous float32 CUDA tensor [..., rows, cols]; 32-blocks along rows ->
-    (codes [..., rows, cols], scales [..., rows/32, cols])."""
+    (codes [..., rows, cols] (FMT_E3M2_BLK: [..., rows/32, cols, 24]), scales [..., rows/32, cols])."""
     import torch
     assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
     rows, cols = x.shape[-2], x.shape[-1]
     mats = x.numel() // (rows * cols)
-    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    cshape = tuple(x.shape[:-2]) + (rows // 32, cols, 24) if fmt == FMT_E3M2_BLK else x.shape
+    codes = torch.empty(cshape, dtype=torch.uint8, device=x.device)
     scales = torch.empty(tuple(x.shape[:-2]) + (rows // 32, cols), dtype=torch.uint8, device=x.device)
     _check(lib().mxfa_quantize_cols(_ptr(x), mats, rows, cols, fmt, _ptr(codes), _ptr(scales), _stream(stream)))
     return codes, scales
+
+
+# Block-packed E3M2: rows 8g + 4a + b (g < 4, a < 2, b < 4) of a 32-row block sit at 6-bit
+# field 16a + 4g + b, i.e. the group of four rows 4q .. 4q + 3 fills bytes 3u .. 3u + 2 with
+# u = 4 (q % 2) + q // 2 -- the key order in which the attention kernels' P operand meets the
+# MFMA's fp6 V operand.
+_BLK_UNIT_GROUP = [2 * (u % 4) + u // 4 for u in range(8)]      # 3-byte unit u <- row group q
+_BLK_GROUP_UNIT = [4 * (q % 2) + q // 2 for q in range(8)]      # row group q -> 3-byte unit u
+
+
+def blk_field(r):
+    """6-bit field of row r (0..31) in a block-packed E3M2 block."""
+    return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3)
+
+
+def e3m2_to_blk(codes):
+    """Host (numpy) repacking of E3M2 codes one per byte, [..., rows, cols] with rows % 32 == 0,
+    into the FMT_E3M2_BLK layout [..., rows/32, cols, 24]: row r of a 32-row block in bits
+    6f .. 6f+5, f = blk_field(r), of its column's 24 bytes read as a 192-bit little-endian
+    integer."""
+    import numpy as np
+    c = np.asarray(codes, dtype=np.uint8)
+    *lead, rows, cols = c.shape
+    c = (c & 0x3F).reshape(*lead, rows // 32, 8, 4, cols)[..., _BLK_UNIT_GROUP, :, :]
+    c = np.moveaxis(c, -1, -3).astype(np.uint32)                        # [..., rows/32, cols, unit, 4]
+    w = c[..., 0] | (c[..., 1] << 6) | (c[..., 2] << 12) | (c[..., 3] << 18)
+    out = np.stack([w & 0xFF, (w >> 8) & 0xFF, (w >> 16) & 0xFF], axis=-1).astype(np.uint8)
+    return out.reshape(*lead, rows // 32, cols, 24)
+
+
+def e3m2_from_blk(blk):
+    """Inverse of e3m2_to_blk: [..., nb, cols, 24] -> E3M2 codes one per byte [..., 32 nb, cols]."""
+    import numpy as np
+    b = np.asarray(blk, dtype=np.uint8)
+    *lead, nb, cols, _ = b.shape
+    b = b.reshape(*lead, nb, cols, 8, 3).astype(np.uint32)[..., _BLK_GROUP_UNIT, :]
+    w = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16)
+    c = np.stack([(w >> (6 * i)) & 0x3F for i in range(4)], axis=-1)   # [..., nb, cols, group, 4]
+    c = np.moveaxis(c.reshape(*lead, nb, cols, 32), -2, -1)            # [..., nb, 32, cols]
+    return c.reshape(*lead, nb * 32, cols).astype(np.uint8)
 
 
 def softmax_requant(s, row_max, c, p_rule=P_R1, stream=None):
@@ -252,8 +294,8 @@ def fill_normal(x, seed, outlier_p=0.0, outlier_mul=20.0, stream=None):
 
 def prefill_plan(p):
     """Workspace bytes of mxfa_prefill_ws for p: the bf16 copy of K (B * Hkv * Sk * D * 2
-    bytes), plus the E4M3 copy of V (B * Hkv * Sk * D bytes) when V is E3M2.  Never 0: every
-    shape runs the workspace kernel."""
+    bytes), plus the E4M3 copy of V (B * Hkv * Sk * D bytes) when V is FMT_E3M2 (block-packed
+    FMT_E3M2_BLK V is read as it is).  Never 0."""
     ws = ctypes.c_size_t(0)
     _check(lib().mxfa_prefill_plan(ctypes.byref(p), ctypes.byref(ws)))
     return ws.value
@@ -349,7 +391,8 @@ class KvCache:
         self.params = KvParams(B, H, D, L, v_fmt)
         self.k = torch.zeros((B, H, L, D), dtype=torch.uint8, device=device)
         self.ks = torch.zeros((B, H, L, D // 32), dtype=torch.uint8, device=device)
-        self.v = torch.zeros((B, H, L, D), dtype=torch.uint8, device=device)
+        vshape = (B, H, L // 32, D, 24) if v_fmt == FMT_E3M2_BLK else (B, H, L, D)
+        self.v = torch.zeros(vshape, dtype=torch.uint8, device=device)
         self.vs = torch.zeros((B, H, L // 32, D), dtype=torch.uint8, device=device)
         self.tail = torch.zeros((B, H, 32, D), dtype=torch.float32, device=device)
         self.length = 0
