@@ -35,11 +35,16 @@ def decode_config():
 
 
 # The other prefill configs of BASELINE.json (timed for the roofline table; the headline is
-# configs[2]).  N(0,1) inputs; c4 is the gemma variant (window, softcap, E3M2 V).
+# configs[2]).  N(0,1) inputs; c4 is the gemma variant (window, softcap, E3M2 V), timed with V
+# block-packed (FMT_E3M2_BLK: the same E3M2 codes and scales, stored as the MFMA's fp6 operand)
+# and, as c4_e3m2_bytes, with the codes one per byte.
 OTHER_CONFIGS = {
     "c1": dict(B=1, Hq=1, Hkv=1, S=256, D=64, causal=False, outlier_p=0.0),
     "c2": dict(B=4, Hq=16, Hkv=16, S=2048, D=128, causal=True, outlier_p=0.0),
-    "c4": dict(B=1, Hq=16, Hkv=8, S=8192, D=256, causal=True, outlier_p=0.0, window=4096, softcap=50.0, v_e3m2=True),
+    "c4": dict(B=1, Hq=16, Hkv=8, S=8192, D=256, causal=True, outlier_p=0.0, window=4096, softcap=50.0,
+               v_fmt=2),                                            # mxfa.FMT_E3M2_BLK
+    "c4_e3m2_bytes": dict(B=1, Hq=16, Hkv=8, S=8192, D=256, causal=True, outlier_p=0.0, window=4096, softcap=50.0,
+                          v_e3m2=True),
 }
 
 
@@ -61,8 +66,9 @@ def make_prefill(torch, mxfa, c, seed=1):
 
 
 def bench_other_configs(torch, mxfa, args):
-    """configs[0], [1], [3]: TFLOP/s and the roofline fraction max(F/P_mfma, B/BW_hbm) / t,
-    B = codes + scales read once + fp32 O written once (E3M2 V counted at 6 bits)."""
+    """configs[0], [1], [3]: TFLOP/s of mxfa_prefill_ws and the roofline fraction max(F/P_mfma,
+    B/BW_hbm) / t, B = codes + scales read once + fp32 O written once (E3M2 V counted at 6
+    bits); the workspace-free entry point (mxfa_prefill) timed beside it."""
     res = {}
     for name, c in OTHER_CONFIGS.items():
         p, ops = make_prefill(torch, mxfa, c, seed=7)
@@ -70,6 +76,9 @@ def bench_other_configs(torch, mxfa, args):
         ws = prefill_workspace(torch, mxfa, p)
         ms = time_calls(torch, lambda: mxfa.prefill(p, *ops, out=out, workspace=ws), max(20, args.steps // 4),
                         args.warmup)
+        # the workspace-free entry point (mxfa_prefill) on the same operands
+        ms_nw = time_calls(torch, lambda: mxfa.prefill(p, *ops, out=out, workspace=False), max(20, args.steps // 4),
+                           args.warmup)
         flops = mxfa.attention_flops(p)
         vbytes = ops[4].numel() * (0.75 if p.v_fmt == mxfa.FMT_E3M2 else 1.0)   # block-packed: 6 bits already
         nbytes = sum(t.numel() for t in (ops[0], ops[1], ops[2], ops[3], ops[5])) + vbytes + out.numel() * 4
@@ -79,6 +88,7 @@ def bench_other_configs(torch, mxfa, args):
                               + (" causal" if c["causal"] else "") + (f" window={c['window']}" if c.get("window") else "")
                               + (f" softcap={c['softcap']}" if c.get("softcap") else "") + {mxfa.FMT_E3M2: " V=E3M2", mxfa.FMT_E3M2_BLK: " V=E3M2 block-packed"}.get(p.v_fmt, ""),
                      "ms_per_call": round(ms, 4), "tflops": round(flops / t / 1e12, 1),
+                     "workspace_free": {"ms_per_call": round(ms_nw, 4), "tflops": round(flops / (ms_nw * 1e-3) / 1e12, 1)},
                      "gflop": round(flops / 1e9, 3), "mb": round(nbytes / 1e6, 1), "roofline_frac": round(frac, 4)}
         del ops, out, ws
     return res
