@@ -507,6 +507,9 @@ def main():
         kd, ksd = mxfa.quantize_rows(Kd)
         mxfa.fill_normal(Kd, 13)
         vd, vsd = mxfa.quantize_cols(Kd)
+        # the same V as MXFP6 E3M2, codes one per byte and block-packed
+        v3, v3s = mxfa.quantize_cols(Kd, mxfa.FMT_E3M2)
+        vb, vbs = mxfa.quantize_cols(Kd, mxfa.FMT_E3M2_BLK)
         del Kd
         pd = mxfa.make_params(dc["B"], dc["Hq"], dc["Hkv"], 1, dc["L"], dc["D"], causal=True, q_pos0=dc["L"] - 1)
         _, ws_bytes = mxfa.decode_plan(pd)
@@ -519,6 +522,17 @@ def main():
         result["decode"] = {"workload": "configs[4]: decode B=64 Hq=32 Hkv=8 D=128 KV length 8192, E4M3 MX KV cache",
                             "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(msd, 4),
                             "bytes_per_call": nbytes, "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        # E3M2 V at the same shape: bytes moved per call with the codes one per byte and with
+        # them block-packed (6 bits, read by the MFMA as they are)
+        for key, fmt, vv, vvs in (("v_e3m2_bytes", mxfa.FMT_E3M2, v3, v3s), ("v_e3m2_blk", mxfa.FMT_E3M2_BLK, vb, vbs)):
+            pv = mxfa.make_params(dc["B"], dc["Hq"], dc["Hkv"], 1, dc["L"], dc["D"], causal=True, q_pos0=dc["L"] - 1,
+                                  v_fmt=fmt)
+            msv = time_calls(torch, lambda: mxfa.decode(pv, qd, qsd, kd, ksd, vv, vvs, out=od, workspace=ws),
+                             args.steps * 5, args.warmup)
+            nbv = sum(t.numel() for t in (qd, qsd, kd, ksd, vv, vvs)) + od.numel() * 4
+            result["decode"][key] = {"ms_per_call": round(msv, 4), "bytes_per_call": nbv,
+                                     "value": round(nbv / (msv * 1e-3) / 1e9, 1), "unit": "GB/s"}
+        del v3, v3s, vb, vbs
 
     if not args.no_decode:
         result["decode"]["hbm_copy_gbs"] = hbm_copy_gbs(torch)

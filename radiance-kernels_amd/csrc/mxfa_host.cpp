@@ -70,6 +70,10 @@ const char* const kKernelNames[] = {
       "mxfa_prefill3_d" #D "_softcap_r2_blk", "mxfa_prefill3n_d" #D "_blk", "mxfa_prefill3n_d" #D "_softcap_blk", \
       "mxfa_prefill3n_d" #D "_r2_blk", "mxfa_prefill3n_d" #D "_softcap_r2_blk"
     MXFA_BLK_NAMES(64), MXFA_BLK_NAMES(128), MXFA_BLK_NAMES(256),
+#define MXFA_DECODE_BLK_NAMES(D)                                                            \
+  "mxfa_decode_d" #D "_blk", "mxfa_decode_d" #D "_softcap_blk", "mxfa_decode_d" #D "_r2_blk", \
+      "mxfa_decode_d" #D "_softcap_r2_blk"
+    MXFA_DECODE_BLK_NAMES(64), MXFA_DECODE_BLK_NAMES(128), MXFA_DECODE_BLK_NAMES(256),
 };
 constexpr int kNumKernels = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
 
@@ -187,7 +191,6 @@ mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
     return fail(MXFA_ERR_INVALID_ARG, "kv_stride must be 0 or a multiple of 32 that is >= seq_k");
   if (decode) {
     if (p->seq_q != 1) return fail(MXFA_ERR_INVALID_ARG, "decode needs seq_q == 1");
-    if (p->v_fmt == MXFA_FMT_E3M2_BLK) return fail(MXFA_ERR_UNSUPPORTED, "decode reads V as E4M3 or E3M2 codes, not E3M2_BLK");
     if (p->num_q_heads / p->num_kv_heads > 32)
       return fail(MXFA_ERR_UNSUPPORTED, "decode supports at most 32 query heads per KV head");
   }
@@ -669,7 +672,8 @@ mxfa_status decode_launch(DeviceModule* dm, const mxfa_attn_params* p, const uin
   const bool force_kernel = comb && std::strcmp(comb, "kernel") == 0;
   a.fuse_combine = !force_kernel && p->head_dim <= 128 && nw % nparts == 0 && a.group <= 16;
   void* args[] = {&a};
-  if (mxfa_status st = launch(dm, kernel_name("decode", p), grid, dim3(64 * nw), args, stream))
+  if (mxfa_status st = launch(dm, kernel_name("decode", p, p->v_fmt == MXFA_FMT_E3M2_BLK), grid, dim3(64 * nw), args,
+                              stream))
     return st;
   if (a.fuse_combine) return MXFA_OK;
   return launch(dm, "mxfa_decode_combine", dim3((unsigned)nbh), dim3((unsigned)p->head_dim), args, stream);

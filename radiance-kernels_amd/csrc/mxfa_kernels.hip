@@ -598,7 +598,9 @@ __device__ __forceinline__ void qk_tiles(v16f (&s)[BN / 32], const v4i* qb, cons
 
 // Softmax, P requant and O^T += V^T P^T for one key block whose scores are in s.
 // mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
-template <int D, bool SOFTCAP, int PR>
+// VBLK: the V tile is block-packed E3M2 as the caller stores it (two 32-key blocks of D
+// columns x 24 bytes), read as the fp6 operand; else E4M3 codes [key][KP].
+template <int D, bool SOFTCAP, int PR, bool VBLK = false>
 __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32], const uint8_t* sV,
                                            const uint8_t* sVs, int key0, int klo, int khi, bool mask,
                                            const FaArgs& a, int lane) {
@@ -683,6 +685,21 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32],
       for (int i = 0; i < 16; i++) st.o[dt][i] *= corr;
   }
 
+  if constexpr (VBLK) {
+    static_assert(BN == 64, "one 64-key PV step");
+    // lane (d, h) reads the 24 bytes of column 32 dt + r of 32-key block h: three ds_read_b64,
+    // lanes 24 bytes apart (32 distinct even banks)
+    const int pscale = psc[h];
+    const uint8_t* a0 = sV + h * (24 * D) + 24 * r;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) {
+      const v2i* src = reinterpret_cast<const v2i*>(a0 + 768 * dt);
+      const v2i x0 = src[0], x1 = src[1], x2 = src[2];
+      const v8i va = (v8i){x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], 0, 0};
+      st.o[dt] = mfma_mx_a6(va, pb[0], st.o[dt], sVs[h * D + dt * 32 + r], pscale);
+    }
+    return;
+  }
   const int l16 = lane & 15, g16 = lane >> 4;
 #pragma unroll
   for (int kstep = 0; kstep < BN / 64; kstep++) {
@@ -707,13 +724,13 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32],
 }
 
 // One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
-template <int D, bool SOFTCAP, int PR>
+template <int D, bool SOFTCAP, int PR, bool VBLK = false>
 __device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
                                            const uint8_t* sVs, int key0, int klo, int khi, bool mask,
                                            const FaArgs& a, int lane) {
   v16f s[BN / 32];
   qk_tiles<D>(s, qb, sKb, lane);
-  softmax_pv<D, SOFTCAP, PR>(st, s, sV, sVs, key0, klo, khi, mask, a, lane);
+  softmax_pv<D, SOFTCAP, PR, VBLK>(st, s, sV, sVs, key0, klo, khi, mask, a, lane);
 }
 
 // Q operand (B of S^T = K Q^T, bf16) for query row `qrow` (zeros if invalid): MFMA kk
@@ -1655,12 +1672,13 @@ MXFA_PREFILL3_TRACE(256, true, P_R2, mxfa_prefill3_trace_d256_softcap_r2)
 // ds_read_b64_tr_b8 reads of the PV step.  Small per-wave LDS and register footprints
 // give two workgroups per CU, whose waves hide each other's load latency.
 // ---------------------------------------------------------------------------
-template <int D, bool SOFTCAP, int PR>
+template <int D, bool SOFTCAP, int PR, bool VBLK = false>
 __device__ void decode_split_impl(const FaArgs& a) {
   constexpr int NW = 4;
   constexpr int NT = BN / 32;
   constexpr int CPR = D / 16;                         // 16-byte chunks per V row
-  constexpr int PERW = BN * CPR / 64;                 // V chunks per lane
+  constexpr int PERW = BN * CPR / 64;                 // K (and E4M3 V) chunks per lane
+  constexpr int PERWV = VBLK ? 3 * D / 64 : PERW;     // V chunks per lane (block-packed: 48 D bytes)
   constexpr int SCW = BN * D / 32 / 4;                // V scale dwords per block
   constexpr int KC = D / 32;                          // 16-byte K chunks per lane per tile
   constexpr int KP = Lds<D>::KP;
@@ -1690,7 +1708,9 @@ __device__ void decode_split_impl(const FaArgs& a) {
   // buffer resources end at Sk: rows past it read 0
   const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.k, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D);
   const __amdgpu_buffer_rsrc_t rks = buf_rsrc(a.ks, (int64_t)bk * a.Skc * (D / 32), (int64_t)a.Sk * (D / 32));
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.v, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D);
+  const __amdgpu_buffer_rsrc_t rv =
+      VBLK ? buf_rsrc(a.v, (int64_t)bk * (a.Skc / 32) * (24 * D), (int64_t)(a.Sk / 32) * (24 * D))
+           : buf_rsrc(a.v, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D);
   const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(a.vs, (int64_t)bk * (a.Skc / 32) * D, (int64_t)(a.Sk / 32) * D);
 
   int klo, khi;
@@ -1743,14 +1763,17 @@ __device__ void decode_split_impl(const FaArgs& a) {
         ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, so, 0, 0);
     }
   };
-  // V codes and scales of a block (stored to the wave's LDS slot after its scores)
-  v4i vr[PERW];
+  // V codes and scales of a block (stored to the wave's LDS slot after its scores); block-
+  // packed V: the block's 48 D contiguous bytes, chunk c at byte 16 c of the slot
+  v4i vr[PERWV];
   uint32_t vsr;
   auto load_v = [&](int key0, bool on) {
 #pragma unroll
-    for (int i = 0; i < PERW; i++) {
+    for (int i = 0; i < PERWV; i++) {
       const int c = lane + 64 * i;
-      const uint32_t vo = on ? (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16) : 0x80000000u;
+      const uint32_t vo = !on ? 0x80000000u
+                          : VBLK ? (uint32_t)((key0 / 32) * (24 * D) + 16 * c)
+                                 : (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16);
       vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kNonTemporal);
     }
     const uint32_t so = on && lane < SCW ? (uint32_t)((key0 / 32) * D + 4 * lane) : 0x80000000u;
@@ -1796,21 +1819,21 @@ __device__ void decode_split_impl(const FaArgs& a) {
     }
     __asm__ volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < PERW; i++) {
+    for (int i = 0; i < PERWV; i++) {
       const int c = lane + 64 * i;
       v4i zv = vr[i];
-      if (a.v_e3m2) {
+      if (!VBLK && a.v_e3m2) {
 #pragma unroll
         for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
       }
-      *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = zv;
+      *reinterpret_cast<v4i*>(&sV[wave][VBLK ? 16 * c : (c / CPR) * KP + (c % CPR) * 16]) = zv;
     }
     if (lane < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * lane]) = vsr;
     load_v(key0 + kstride, key0 + kstride < klast);
     // LDS operations of one wave complete in order: the V tile written above is in place
     // for the transposed reads, and the next block's writes follow this block's reads
     const bool mask = key0 < klo_u || key0 + BN - 1 > khi_u;
-    softmax_pv<D, SOFTCAP, PR>(st, sc, sV[wave], sVs[wave], key0, klo, khi, mask, a, lane);
+    softmax_pv<D, SOFTCAP, PR, VBLK>(st, sc, sV[wave], sVs[wave], key0, klo, khi, mask, a, lane);
   }
 
   float l = pair_sum(st.l);
@@ -1898,7 +1921,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
 // Waves per decode workgroup (each wave has private LDS tiles).
 template <int D> struct DecodeWaves { static constexpr int N = D == 256 ? 2 : 4; };
 
-template <int D, bool SOFTCAP, int PR>
+template <int D, bool SOFTCAP, int PR, bool VBLK = false>
 __device__ void decode_impl(const FaArgs& a) {
   constexpr int NW = DecodeWaves<D>::N;
   __shared__ __attribute__((aligned(16))) uint8_t sK[NW][Lds<D>::TILEK];
@@ -1920,7 +1943,7 @@ __device__ void decode_impl(const FaArgs& a) {
 
   const uint8_t* kb = a.k + (int64_t)bk * a.Skc * D;
   const uint8_t* ksb = a.ks + (int64_t)bk * a.Skc * (D / 32);
-  const uint8_t* vb = a.v + (int64_t)bk * a.Skc * D;
+  const uint8_t* vb = a.v + (int64_t)bk * (VBLK ? (a.Skc / 32) * (24 * D) : (int64_t)a.Skc * D);
   const uint8_t* vsb = a.vs + (int64_t)bk * (a.Skc / 32) * D;
 
   // partial `part` of n_qblk takes the key blocks part, part + n_qblk, ...
@@ -1949,10 +1972,10 @@ __device__ void decode_impl(const FaArgs& a) {
       uint32_t ksc = 0;
       if (key < kend) {
         zk = *reinterpret_cast<const v4i*>(kb + (int64_t)key * D + col);
-        zv = *reinterpret_cast<const v4i*>(vb + (int64_t)key * D + col);
+        if (!VBLK) zv = *reinterpret_cast<const v4i*>(vb + (int64_t)key * D + col);
         ksc = ksb[(int64_t)key * (D / 32) + col / 32];
       }
-      if (a.v_e3m2) {
+      if (!VBLK && a.v_e3m2) {
 #pragma unroll
         for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
       }
@@ -1961,7 +1984,19 @@ __device__ void decode_impl(const FaArgs& a) {
       v4i b1 = fp8x8_to_bf16x8((uint32_t)zk[2], (uint32_t)zk[3], sc);
       *reinterpret_cast<v4i*>(&sK[wave][row * KPB + col * 2]) = b0;
       *reinterpret_cast<v4i*>(&sK[wave][row * KPB + col * 2 + 16]) = b1;
-      *reinterpret_cast<v4i*>(&sV[wave][row * KP + col]) = zv;
+      if (!VBLK) *reinterpret_cast<v4i*>(&sV[wave][row * KP + col]) = zv;
+    }
+    if constexpr (VBLK) {
+      // the block's 48 D bytes as they are (a 32-key block past Sk reads 0)
+#pragma unroll
+      for (int i = 0; i < 3 * D / 64; i++) {
+        const int c = lane + 64 * i;
+        const int kb32 = 16 * c / (24 * D);
+        v4i zv = {0, 0, 0, 0};
+        if (key0 + 32 * kb32 < kend)
+          zv = *reinterpret_cast<const v4i*>(vb + (int64_t)(key0 / 32) * (24 * D) + 16 * c);
+        *reinterpret_cast<v4i*>(&sV[wave][16 * c]) = zv;
+      }
     }
     constexpr int SCW = BN * D / 32 / 4;   // V scale dwords per block
     for (int i = lane; i < SCW; i += 64) {
@@ -1973,7 +2008,7 @@ __device__ void decode_impl(const FaArgs& a) {
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     // columns >= group are padding and must be masked
-    wave_block<D, SOFTCAP, PR>(st, qb, sK[wave], sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
+    wave_block<D, SOFTCAP, PR, VBLK>(st, qb, sK[wave], sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
     __builtin_amdgcn_wave_barrier();
   }
 
@@ -2019,6 +2054,24 @@ MXFA_DECODE(256, false, P_R2, mxfa_decode_d256_r2)
 MXFA_DECODE_SPLIT(64, true, P_R2, mxfa_decode_d64_softcap_r2)
 MXFA_DECODE_SPLIT(128, true, P_R2, mxfa_decode_d128_softcap_r2)
 MXFA_DECODE(256, true, P_R2, mxfa_decode_d256_softcap_r2)
+// block-packed E3M2 V (read as the fp6 operand)
+#define MXFA_DECODE_BLK(D, SC, PR, NAME)                                                \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC, PR, true>(a); }
+#define MXFA_DECODE256_BLK(SC, PR, NAME)                                                \
+  extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<256>::N) NAME(FaArgs a) { \
+    decode_impl<256, SC, PR, true>(a);                                                  \
+  }
+#define MXFA_DECODE_BLK_ALL(D)                                                 \
+  MXFA_DECODE_BLK(D, false, P_R1, mxfa_decode_d##D##_blk)                     \
+  MXFA_DECODE_BLK(D, true, P_R1, mxfa_decode_d##D##_softcap_blk)              \
+  MXFA_DECODE_BLK(D, false, P_R2, mxfa_decode_d##D##_r2_blk)                  \
+  MXFA_DECODE_BLK(D, true, P_R2, mxfa_decode_d##D##_softcap_r2_blk)
+MXFA_DECODE_BLK_ALL(64)
+MXFA_DECODE_BLK_ALL(128)
+MXFA_DECODE256_BLK(false, P_R1, mxfa_decode_d256_blk)
+MXFA_DECODE256_BLK(true, P_R1, mxfa_decode_d256_softcap_blk)
+MXFA_DECODE256_BLK(false, P_R2, mxfa_decode_d256_r2_blk)
+MXFA_DECODE256_BLK(true, P_R2, mxfa_decode_d256_softcap_r2_blk)
 
 // Merge nparts partials per (b, query head) in part order: O = sum_i O_i 2^{(m_i - M) c} / sum_i l_i 2^{(m_i - M) c}.
 // One workgroup of D threads per query head.

@@ -158,17 +158,83 @@ def test_kv_append_blk_matches_one_shot_then_prefill():
     assert torch.equal(got, ref)
 
 
-def test_decode_and_trace_refuse_blk():
-    """Decode and the stage trace read V as codes one per byte: block-packed V is refused
-    with MXFA_ERR_UNSUPPORTED before anything is launched."""
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,softcap,p_rule,window", [
+    (3, 8, 2, 480, 64, 0.0, mxfa.P_R1, 0),          # ragged last block (L % 64 = 32)
+    (4, 32, 8, 1056, 128, 0.0, mxfa.P_R1, 0),       # ragged: the second 32-key block of the last is past L
+    (2, 16, 8, 2080, 256, 30.0, mxfa.P_R1, 0),      # D = 256 kernel, softcap
+    (2, 16, 4, 1024, 128, 50.0, mxfa.P_R2, 300),    # R2, window
+    (1, 8, 8, 800, 256, 0.0, mxfa.P_R2, 0),
+])
+def test_decode_blk_matches_oracle_and_byte_e3m2(B, Hq, Hkv, L, D, softcap, p_rule, window):
+    """Decode over block-packed E3M2 V: the D <= 128 kernel loads each block's 48 D bytes
+    into the wave's LDS slot, the D = 256 kernel per 32-key block up to the sequence end; PV
+    reads them as the fp6 operand.  Against the oracle (codes unpacked) and the byte-E3M2
+    decode (same values: O within a few ulps)."""
+    print(f"blk decode B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} softcap {softcap} p_rule {p_rule} window {window}", flush=True)
+    L32 = -(-L // 32) * 32
+    fp, dev, host = gen_qkv(B, Hq, Hkv, 1, L32, D, 650 + D + L % 97, v_fmt=mxfa.FMT_E3M2)
+    vb, vbs = mxfa.quantize_cols(fp["V"], BLK)
+    kw = dict(causal=True, q_pos0=L - 1, softcap=softcap, p_rule=p_rule, window=window)
+    p = mxfa.make_params(B, Hq, Hkv, 1, L32, D, v_fmt=BLK, **kw)
+    pe = mxfa.make_params(B, Hq, Hkv, 1, L32, D, v_fmt=mxfa.FMT_E3M2, **kw)
+    out = mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], vb, vbs)
+    ref = mxfa.decode(pe, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
+    torch.cuda.synchronize()
+    o = np_(out)
+    assert np.all(np.isfinite(o))
+    n_parts, _ = mxfa.decode_plan(p)
+    want = O.attention(oracle_params(pe), host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"],
+                       block_n=mxfa.DEFAULT_BLOCK_N, n_parts=n_parts)
+    rel, mab = errors(o, want)
+    drel, dmab = errors(o, np_(ref))
+    print(f"   n_parts {n_parts}: rel-L2 {rel:.3e} max-abs {mab:.3e}; vs byte E3M2 rel-L2 {drel:.2e} max-abs "
+          f"{dmab:.2e} (bit-identical: {torch.equal(out, ref)})", flush=True)
+    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+    assert drel <= 1e-5 and dmab <= 1e-4
+
+
+def test_decode_blk_over_appended_cache_and_noalloc():
+    """The serving loop on a block-packed cache: prefill-sized append, then one-token appends
+    with a decode after each (seq_k = length rounded up to 32, kv_stride = max_len); each
+    decode against the oracle on the unpacked cache, and mxfa_decode_noalloc equal to
+    mxfa_decode bit for bit."""
+    B, Hq, H, L, D = 2, 8, 2, 256, 128
+    rng = np.random.default_rng(660)
+    Kf = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    Vf = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    Qf = rng.standard_normal((3, B, Hq, 1, D)).astype(np.float32)
+    cache = mxfa.KvCache(B, H, D, L, v_fmt=BLK)
+    Kd, Vd = torch.from_numpy(Kf).to(DEV), torch.from_numpy(Vf).to(DEV)
+    mxfa.init()
+    for step, n in enumerate([161, 1, 1]):
+        p0 = cache.length
+        cache.append(Kd[:, :, p0:p0 + n].contiguous(), Vd[:, :, p0:p0 + n].contiguous())
+        q, qs = mxfa.quantize_rows(torch.from_numpy(Qf[step]).to(DEV))
+        p = cache.decode_params(Hq)
+        out = mxfa.decode(p, q, qs, cache.k, cache.ks, cache.v, cache.vs)
+        out_na = torch.empty_like(out)
+        mxfa.decode_noalloc(p, q, qs, cache.k, cache.ks, cache.v, cache.vs, out_na)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_na)
+        sk = p.seq_k
+        pe = mxfa.make_params(B, Hq, H, 1, sk, D, causal=True, q_pos0=cache.length - 1, v_fmt=mxfa.FMT_E3M2)
+        n_parts, _ = mxfa.decode_plan(pe)
+        v_bytes = mxfa.e3m2_from_blk(np_(cache.v)[:, :, :sk // 32])
+        c = np.ascontiguousarray
+        want = O.attention(oracle_params(pe), np_(q), np_(qs), c(np_(cache.k)[:, :, :sk]), c(np_(cache.ks)[:, :, :sk]),
+                           v_bytes, c(np_(cache.vs)[:, :, :sk // 32]), block_n=mxfa.DEFAULT_BLOCK_N, n_parts=n_parts)
+        rel, mab = errors(np_(out), want)
+        print(f"   length {cache.length}: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
+        assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+
+
+def test_trace_refuses_blk():
+    """The stage trace reads V as codes one per byte: block-packed V is refused with
+    MXFA_ERR_UNSUPPORTED before anything is launched."""
     B, Hq, Hkv, Sk, D = 1, 2, 1, 64, 64
     z = lambda *s: torch.zeros(s, dtype=torch.uint8, device=DEV)  # noqa: E731
     k, ks = z(B, Hkv, Sk, D), z(B, Hkv, Sk, D // 32)
     v, vs = z(B, Hkv, Sk // 32, D, 24), z(B, Hkv, Sk // 32, D)
-    pd = mxfa.make_params(B, Hq, Hkv, 1, Sk, D, causal=True, q_pos0=Sk - 1, v_fmt=BLK)
-    with pytest.raises(mxfa.MxfaError) as e:
-        mxfa.decode(pd, z(B, Hq, 1, D), z(B, Hq, 1, D // 32), k, ks, v, vs)
-    assert e.value.status == 2
     pp = mxfa.make_params(B, Hq, Hkv, 32, Sk, D, v_fmt=BLK)
     with pytest.raises(mxfa.MxfaError) as e:
         mxfa.prefill_trace(pp, z(B, Hq, 32, D), z(B, Hq, 32, D // 32), k, ks, v, vs, 0, 0)
