@@ -89,7 +89,8 @@ def bench_other_configs(torch, mxfa, args):
                               + (f" softcap={c['softcap']}" if c.get("softcap") else "") + {mxfa.FMT_E3M2: " V=E3M2", mxfa.FMT_E3M2_BLK: " V=E3M2 block-packed"}.get(p.v_fmt, ""),
                      "ms_per_call": round(ms, 4), "tflops": round(flops / t / 1e12, 1),
                      "workspace_free": {"ms_per_call": round(ms_nw, 4), "tflops": round(flops / (ms_nw * 1e-3) / 1e12, 1)},
-                     "gflop": round(flops / 1e9, 3), "mb": round(nbytes / 1e6, 1), "roofline_frac": round(frac, 4)}
+                     "gflop": round(flops / 1e9, 3), "mb": round(nbytes / 1e6, 1), "roofline_frac": round(frac, 4),
+                     "mfma_ceiling": round(mfma_ceiling(mxfa, p, flops)[0], 4)}
         del ops, out, ws
     return res
 
