@@ -293,11 +293,26 @@ def bench_gemm(torch, mxfa, args):
     c16 = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     ms16 = time_calls(torch, lambda: mxfa.gemm(xq, xs, wq, ws, out=c16, c_fmt=mxfa.C_BF16), args.steps, args.warmup)
     tf16 = 2.0 * M * N * K / (ms16 * 1e-3) / 1e12
+    # the same weights at decode batch M = 64 (the skinny kernel: one workgroup per 32-column
+    # strip); HBM-bound on the weights, so reported as the weight stream rate
+    Md = 64
+    Xd = torch.empty((Md, K), dtype=torch.float32, device=dev)
+    mxfa.fill_normal(Xd, 43)
+    xdq, xds = mxfa.quantize_rows(Xd)
+    xds = xds.t().contiguous()
+    cd = torch.empty((Md, N), dtype=torch.float32, device=dev)
+    msd = time_calls(torch, lambda: mxfa.gemm(xdq, xds, wq, ws, out=cd), args.steps, args.warmup)
+    wbytes = wq.numel() + ws.numel()
+    decode_m = {"workload": f"the same weights at decode batch M={Md} (N={N} K={K})", "ms_per_call": round(msd, 4),
+                "weight_bytes": wbytes, "value": round(wbytes / (msd * 1e-3) / 1e9, 1), "unit": "GB/s",
+                "frac_hbm_peak": round(wbytes / (msd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del Xd, xdq, xds, cd
     return {"workload": f"QKV projection of configs[2]: M={M} N={N} K={K}, E4M3 x E4M3 -> fp32",
             "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_call": round(ms, 4),
             "frac_mxfp8_peak": round(tflops / MXFP8_PEAK_TFLOPS, 4),
             "bf16_out": {"value": round(tf16, 1), "unit": "TFLOP/s", "ms_per_call": round(ms16, 4),
-                         "frac_mxfp8_peak": round(tf16 / MXFP8_PEAK_TFLOPS, 4)}}
+                         "frac_mxfp8_peak": round(tf16 / MXFP8_PEAK_TFLOPS, 4)},
+            "decode_batch": decode_m}
 
 
 def cpu_model():

@@ -272,7 +272,10 @@ typedef struct {
  * Replaces the Gemmini MX GEMM driver's tile loop (lib/mxgemm/mxgemm_lib.hpp:11-250) with the
  * scaled MXFP8 MFMA (fp32 accumulation, not Gemmini's narrow accumulators).  The reference's
  * requant output (C_out + C_scales_row, rule R1) is mxfa_quantize_rows applied to c (scales
- * then [M][N/32], the transpose of C_scales_row). */
+ * then [M][N/32], the transpose of C_scales_row).  M <= 128 with E4M3 operands (the
+ * reference's batched-decode projections, kernels/gemv_batched_fp8_m32/64/128) runs a kernel
+ * with one workgroup per 32 columns of C, the k steps split over its waves; every shape gives
+ * the same C run to run. */
 mxfa_status mxfa_gemm(const mxfa_gemm_params *p, const uint8_t *a, const uint8_t *a_sc,
                       const uint8_t *b, const uint8_t *b_sc, void *c, void *stream);
 

@@ -55,7 +55,7 @@ const char* const kKernelNames[] = {
     "mxfa_prefill3_trace_d64_softcap", "mxfa_prefill3_trace_d128_softcap", "mxfa_prefill3_trace_d256_softcap",
     "mxfa_prefill3_trace_d64_r2", "mxfa_prefill3_trace_d128_r2", "mxfa_prefill3_trace_d256_r2",
     "mxfa_prefill3_trace_d64_softcap_r2", "mxfa_prefill3_trace_d128_softcap_r2", "mxfa_prefill3_trace_d256_softcap_r2",
-    "mxfa_gemm_dma",
+    "mxfa_gemm_dma", "mxfa_gemm_skinny_t1", "mxfa_gemm_skinny_t2", "mxfa_gemm_skinny_t4",
     "mxfa_prefill3n_d64", "mxfa_prefill3n_d128", "mxfa_prefill3n_d256", "mxfa_prefill3n_d64_softcap",
     "mxfa_prefill3n_d128_softcap", "mxfa_prefill3n_d256_softcap", "mxfa_prefill3n_d64_r2", "mxfa_prefill3n_d128_r2",
     "mxfa_prefill3n_d256_r2", "mxfa_prefill3n_d64_softcap_r2", "mxfa_prefill3n_d128_softcap_r2",
@@ -446,6 +446,15 @@ mxfa_status mxfa_gemm(const mxfa_gemm_params* p, const uint8_t* a, const uint8_t
   // E4M3 operands with whole K steps (k % 128 == 0) take the LDS-DMA kernel
   // (MXFA_GEMM=reg selects the register-staged one, for comparison).
   const char* sel = getenv("MXFA_GEMM");
+  // M <= 128 with E4M3 operands (the batched-decode projection): the skinny kernel, one
+  // workgroup per 32-column strip (MXFA_GEMM=big or =reg selects the tiled kernels instead)
+  // (its LDS holds all of SA and the strip's SB: (k / 32) (m + 32) <= 96 KiB)
+  if (!g.a_e3m2 && !g.b_e3m2 && p->m <= 128 && (p->k / 32) * (p->m + 32) <= 96 * 1024 &&
+      !(sel && (std::strcmp(sel, "big") == 0 || std::strcmp(sel, "reg") == 0))) {
+    const char* sk = p->m <= 32 ? "mxfa_gemm_skinny_t1" : p->m <= 64 ? "mxfa_gemm_skinny_t2" : "mxfa_gemm_skinny_t4";
+    void* args[] = {&g};
+    return launch(dm, sk, dim3((unsigned)((p->n + 31) / 32)), dim3(256), args, stream);
+  }
   const bool dma = !g.a_e3m2 && !g.b_e3m2 && p->k % 128 == 0 && !(sel && std::strcmp(sel, "reg") == 0);
   const char* name = dma ? "mxfa_gemm_dma" : names[g.a_e3m2][g.b_e3m2];
   int threads = 0;

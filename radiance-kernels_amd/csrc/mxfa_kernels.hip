@@ -37,6 +37,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "mx_device.h"
 #include "mxfa_args.h"
@@ -2568,6 +2569,190 @@ __device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
 }
 
 extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_dma(GemmArgs g) { gemm_dma_impl<8>(g); }
+
+// ---------------------------------------------------------------------------
+// Skinny MX GEMM (M <= 32 T rows, E4M3 x E4M3): the batched-decode projection, where the big
+// kernel's 256 x 256 tiles leave the chip idle (N / 256 workgroups) and the weights B stream
+// at a few percent of HBM.  One workgroup per 32-column strip of B and C (strips contiguous
+// per XCD, so the four strips that share each 128-byte line of a B row share one L2).  The
+// workgroup first copies all of SA and its strip of SB into LDS ((K / 32) (M + 32) bytes);
+// then its four waves take the 64-k steps w, w + 4, ... and each keeps a ring of R steps of
+// operands in registers, loaded R steps ahead (the loop is unrolled by R, so every ring slot
+// is its own registers and every wait is a partial vmcnt):
+//   B   k rows k0 + 32 q + lane / 2, 16-byte half lane % 2 of the strip (q = 0, 1; columns >= N
+//       read 0), written to the wave's 2 KB LDS slab [64 k][32] for the transposed reads
+//   A   row 32 i + lane % 32, bytes k0 + 16 h .. and k0 + 32 + 16 h .. (h = lane / 32): the MFMA
+//       operand as it is (rows >= M read 0)
+// The four partial accumulators are summed through LDS in wave order (deterministic) and C
+// is stored 32 consecutive columns per 32 lanes.
+// ---------------------------------------------------------------------------
+constexpr int SKINNY_SCALE_BYTES = 96 * 1024;                   // (K / 32) (M + 32) at most
+
+// Ring slots (steps in flight per wave).  Measured on M = 16 / 64 / 128 (N 6144, K 4096): 8 / 6 /
+// 4 slots 11.3 / 17.0 / 25.7 us, the vmcnt limit (16 / 11 / 7) 14.1 / 18.2 / 26.4 us.
+template <int T> struct SkinnyCfg {
+  static constexpr int R = T == 1 ? 8 : T == 2 ? 6 : 4;
+  static_assert((R - 1) * (2 + 2 * T) <= 63, "vmcnt range");
+};
+
+template <int T> struct SkinnySlot {
+  v4i b[2];
+  v4i a[T][2];
+};
+
+// Offsets of a disabled load get bit 31 set (arithmetic, not a select: a uniform condition
+// would otherwise become a branch around the load), which puts them past every resource.
+template <int T>
+__device__ __forceinline__ void skinny_load(SkinnySlot<T>& sl, const GemmArgs& g, __amdgpu_buffer_rsrc_t ra,
+                                            __amdgpu_buffer_rsrc_t rb, int step, bool on, int n0, int lane) {
+  const int r = lane & 31, h = lane >> 5, k0 = step * 64;
+  const uint32_t dis = (uint32_t)!on << 31;
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int col = n0 + 16 * (lane & 1);
+    const uint32_t vo = (uint32_t)((k0 + 32 * q + (lane >> 1)) * g.N + col) | dis | ((uint32_t)(col >= g.N) << 31);
+    sl.b[q] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < T; i++) {
+    const int row = 32 * i + r;
+    const uint32_t vo = (uint32_t)(row * g.K + k0 + 16 * h) | dis | ((uint32_t)(row >= g.M) << 31);
+    sl.a[i][0] = __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0);
+    sl.a[i][1] = __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 32, 0, 0);
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void skinny_mma(v16f (&acc)[T], const SkinnySlot<T>& sl, uint8_t* slab,
+                                           const uint8_t* ssa, const uint8_t* ssb, int M, int step, int lane) {
+  const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
+  // B slab [64 k][32 columns]: this lane's two 16-byte pieces, then the transposed reads
+  // (one wave's LDS operations complete in order, so the previous step's reads are done)
+  *reinterpret_cast<v4i*>(slab + 16 * lane) = sl.b[0];
+  *reinterpret_cast<v4i*>(slab + 1024 + 16 * lane) = sl.b[1];
+  v8i bo;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int krow = 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
+    const v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(slab + krow * 32 + 16 * (g16 & 1) + 8 * (l16 & 1)));
+    bo[2 * q] = t[0];
+    bo[2 * q + 1] = t[1];
+  }
+  const int sb = ssb[(2 * step + h) * 32 + r];
+#pragma unroll
+  for (int i = 0; i < T; i++)
+    acc[i] = mfma_mx(cat44(sl.a[i][0], sl.a[i][1]), bo, acc[i], ssa[(2 * step + h) * M + 32 * i + r], sb);
+}
+
+template <int T, int... J>
+__device__ __forceinline__ void skinny_round(v16f (&acc)[T], SkinnySlot<T> (&ring)[SkinnyCfg<T>::R], const GemmArgs& g,
+                                             __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, uint8_t* slab,
+                                             const uint8_t* ssa, const uint8_t* ssb, int step0, int nsteps, int n0,
+                                             int lane, std::integer_sequence<int, J...>) {
+  constexpr int R = SkinnyCfg<T>::R;
+  // slot J: multiply step step0 + 4 J, then load step step0 + 4 (J + R) into it (past the last
+  // step the loads read nothing; no branch, so the waits stay partial)
+  ((skinny_mma<T>(acc, ring[J], slab, ssa, ssb, g.M, step0 + 4 * J, lane),
+    skinny_load<T>(ring[J], g, ra, rb, step0 + 4 * (J + R), step0 + 4 * (J + R) < nsteps, n0, lane),
+    __builtin_amdgcn_sched_barrier(0)),
+   ...);
+}
+
+template <int T, int... J>
+__device__ __forceinline__ void skinny_tail(v16f (&acc)[T], SkinnySlot<T> (&ring)[SkinnyCfg<T>::R], uint8_t* slab,
+                                            const uint8_t* ssa, const uint8_t* ssb, int M, int step0, int left,
+                                            int lane, std::integer_sequence<int, J...>) {
+  ((J < left ? (skinny_mma<T>(acc, ring[J], slab, ssa, ssb, M, step0 + 4 * J, lane), 0) : 0), ...);
+}
+
+template <int T>
+__device__ void gemm_skinny_impl(const GemmArgs& g) {
+  constexpr int R = SkinnyCfg<T>::R;
+  __shared__ __attribute__((aligned(16))) uint8_t slabs[4 * 2048];
+  __shared__ __attribute__((aligned(16))) uint8_t scales[SKINNY_SCALE_BYTES];
+  __shared__ __attribute__((aligned(16))) float part[4 * 16 * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nstrips = (g.N + 31) / 32;
+  const int nwg = (int)gridDim.x, lin = (int)blockIdx.x;
+  const int xcd = lin & 7, per = nwg >> 3, rem = nwg & 7;
+  const int strip = xcd * per + min(xcd, rem) + (lin >> 3);
+  if (strip >= nstrips) return;                                   // whole workgroups leave together
+  const int n0 = 32 * strip;
+  const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, 0, (int64_t)g.M * g.K);
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, 0, (int64_t)g.K * g.N);
+  const int nsteps = g.K / 64, kb = g.K / 32;
+  uint8_t* const slab = slabs + 2048 * wave;
+  uint8_t* const ssa = scales;                                     // [K / 32][M]
+  uint8_t* const ssb = scales + kb * g.M;                          // [K / 32][32]: the strip's columns
+
+  SkinnySlot<T> ring[R];
+#pragma unroll
+  for (int j = 0; j < R; j++) {
+    skinny_load<T>(ring[j], g, ra, rb, wave + 4 * j, wave + 4 * j < nsteps, n0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  {
+    // the scales, in batches of 8 dwords per thread (all loads of a batch before its stores;
+    // M % 16 == 0 and N % 16 == 0 keep every dword aligned): SA whole, then the strip's 32
+    // bytes of each SB row (columns >= N read 0)
+    const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(g.sa, 0, (int64_t)kb * g.M);
+    const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(g.sb, 0, (int64_t)kb * g.N);
+    const int na = kb * g.M / 4, nb = kb * 8;
+    for (int base = tid; base < na + nb; base += 256 * 8) {
+      uint32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int d = base + 256 * u;
+        if (d < na) {
+          v[u] = __builtin_amdgcn_raw_buffer_load_b32(rsa, 4 * d, 0, 0);
+        } else {
+          const int e = d - na, row = e >> 3, col = n0 + 4 * (e & 7);
+          const uint32_t so = (uint32_t)(row * g.N + col) | ((uint32_t)(col >= g.N || e >= nb) << 31);
+          v[u] = __builtin_amdgcn_raw_buffer_load_b32(rsb, so, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int d = base + 256 * u;
+        if (d < na + nb) reinterpret_cast<uint32_t*>(scales)[d] = v[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  v16f acc[T];
+#pragma unroll
+  for (int i = 0; i < T; i++) acc[i] = (v16f){};
+  // this wave's steps: wave, wave + 4, ...; full rounds of R, then the last < R from the ring
+  const int mine = nsteps > wave ? (nsteps - wave + 3) / 4 : 0;
+  int step0 = wave;
+  for (int round = 0; round < mine / R; round++, step0 += 4 * R)
+    skinny_round<T>(acc, ring, g, ra, rb, slab, ssa, ssb, step0, nsteps, n0, lane, std::make_integer_sequence<int, R>{});
+  skinny_tail<T>(acc, ring, slab, ssa, ssb, g.M, step0, mine % R, lane, std::make_integer_sequence<int, R - 1>{});
+  // the four partials of each row tile, summed in wave order
+#pragma unroll
+  for (int i = 0; i < T; i++) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) part[(wave * 16 + v) * 64 + lane] = acc[i][v];
+    __syncthreads();
+    for (int e = tid; e < 16 * 64; e += 256) {
+      const int v = e / 64, L = e % 64;
+      const float x = ((part[e] + part[1024 + e]) + part[2048 + e]) + part[3072 + e];
+      const int row = 32 * i + 8 * (v >> 2) + 4 * (L >> 5) + (v & 3), col = n0 + (L & 31);
+      if (row < g.M && col < g.N) {
+        if (g.c_bf16)
+          reinterpret_cast<__bf16*>(g.c)[(int64_t)row * g.N + col] = (__bf16)x;
+        else
+          reinterpret_cast<float*>(g.c)[(int64_t)row * g.N + col] = x;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256, 1) mxfa_gemm_skinny_t1(GemmArgs g) { gemm_skinny_impl<1>(g); }
+extern "C" __global__ void __launch_bounds__(256, 1) mxfa_gemm_skinny_t2(GemmArgs g) { gemm_skinny_impl<2>(g); }
+extern "C" __global__ void __launch_bounds__(256, 1) mxfa_gemm_skinny_t4(GemmArgs g) { gemm_skinny_impl<4>(g); }
 
 // Waves per GEMM workgroup; the host reads the workgroup size from the kernel's
 // launch bounds (its maximum threads per block).

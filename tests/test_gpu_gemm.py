@@ -154,3 +154,45 @@ def test_gemm_dma_kernel_equals_register_staged(monkeypatch, M, N, K):
         torch.cuda.synchronize()
         assert bool(torch.isfinite(outs[0]).all())
         assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 64, 64), (32, 96, 1024), (48, 80, 192), (64, 6144, 4096), (96, 208, 576),
+                                   (128, 512, 2048), (112, 48, 4160)])
+def test_gemm_skinny_matches_oracle_and_tiled_kernel(monkeypatch, M, N, K):
+    """M <= 128 with E4M3 operands runs the skinny kernel (one workgroup per 32-column strip, the
+    64-k steps split over its four waves, partials summed in wave order): within the oracle's
+    bound like every mxfa_gemm, close to the tiled kernel (MXFA_GEMM=big: the same products,
+    accumulated in another order), deterministic, fp32 and bf16 C."""
+    print(f"skinny gemm M{M} N{N} K{K}", flush=True)
+    rng = np.random.default_rng(M * 7 + N + K)
+    a, b = _codes(rng, (M, K), 0), _codes(rng, (K, N), 0)
+    sa = rng.integers(112, 142, (K // 32, M)).astype(np.uint8)
+    sb = rng.integers(112, 142, (K // 32, N)).astype(np.uint8)
+    dev = [torch.from_numpy(x).to(DEV) for x in (a, sa, b, sb)]
+    outs = {}
+    for mode in ("skinny", "big"):
+        if mode == "big":
+            monkeypatch.setenv("MXFA_GEMM", "big")
+        c = torch.full((M, N), float("nan"), dtype=torch.float32, device=DEV)
+        mxfa.gemm(*dev, out=c)
+        c16 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+        mxfa.gemm(*dev, out=c16, c_fmt=mxfa.C_BF16)
+        outs[mode] = (c, c16)
+    monkeypatch.delenv("MXFA_GEMM")
+    c2 = torch.empty((M, N), dtype=torch.float32, device=DEV)
+    mxfa.gemm(*dev, out=c2)
+    torch.cuda.synchronize()
+    c, c16 = outs["skinny"]
+    assert torch.equal(c, c2), "not deterministic"
+    assert torch.equal(c16.view(torch.int16), c.to(torch.bfloat16).view(torch.int16)), "bf16 C is not the RNE of fp32 C"
+    want, ab = O.mx_gemm(a, sa, b, sb, mxfa.FMT_E4M3, mxfa.FMT_E4M3, with_abs=True)
+    got = np_(c).astype(np.float64)
+    err = np.abs(got - want)
+    print(f"   rel-L2 {rel_l2(got, want):.2e}, max err / sum|terms| {float((err / np.maximum(ab, 1e-300)).max()):.2e}",
+          flush=True)
+    assert np.all(np.isfinite(got))
+    assert np.all(err <= ab * 2.0 ** -8 + 1e-38)
+    assert rel_l2(got, want) <= 1e-3
+    big = np_(outs["big"][0]).astype(np.float64)
+    # the same products; the partial sums enter the MFMAs' accumulation in another order
+    assert np.all(np.abs(got - big) <= ab * 2.0 ** -12 + 1e-38)
