@@ -341,8 +341,10 @@ mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32
     return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte, codes and scales 4-byte aligned");
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
-  int64_t threads = mats * (rows / 32) * (cols / 4);
-  dim3 grid((unsigned)((threads + 255) / 256));
+  // one wave per (matrix, 32-row block, 128 columns), four waves per workgroup
+  const int64_t units = mats * (rows / 32) * ((cols + 127) / 128);
+  if ((units + 3) / 4 > INT32_MAX) return fail(MXFA_ERR_UNSUPPORTED, "mxfa_quantize_cols: too many 32 x 128 blocks");
+  dim3 grid((unsigned)((units + 3) / 4));
   void* args[] = {(void*)&x, &mats, &rows, &cols, &codes, &scales};
   return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : fmt == MXFA_FMT_E3M2 ? "mxfa_quant_cols_e3m2"
                                                                                         : "mxfa_quant_cols_e3m2_blk",

@@ -116,58 +116,76 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_r4(const float
   if (part == 0) scales[blk] = (uint8_t)sc;
 }
 
-// 32-blocks along rows (V layout): each lane owns 4 adjacent columns of one
-// 32-row block.  mats matrices of rows x cols; rows % 32 == 0, cols % 4 == 0.
+// 32-blocks along rows (V layout).  One wave per (matrix, 32-row block, 128 columns): lane
+// (cg, h) = (lane % 32, lane / 32) owns columns 4 cg .. 4 cg + 3 of the group and the 16 rows
+// 8 g + 4 h + b (g, b < 4), read once into registers (a load instruction covers 512 contiguous
+// bytes of each of two rows); the two row halves combine their amax with one lane swap.
+// mats matrices of rows x cols; rows % 32 == 0, cols % 4 == 0 (columns past cols are skipped).
 // FMT 2: E3M2, each 32-row block of a column stored as 24 bytes at codes + ((m * rows / 32 +
 // rb) * cols + c) * 24, row r's code in field blk6_field(r) (bits 6f .. 6f + 5, little
 // endian): the fp6 A operand of the scaled MFMA in the key order of the P operand the
-// attention kernels build.
+// attention kernels build.  Lane half h's rows are fields 16 h .. 16 h + 15 in row order, i.e.
+// 12 contiguous bytes of each of its columns' blocks.
 template <int FMT>
 __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int rows, int cols,
                                 uint8_t* __restrict__ codes, uint8_t* __restrict__ scales) {
-  int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int cg = cols / 4;
-  int64_t per_mat = (int64_t)(rows / 32) * cg;
-  if (gt >= mats * per_mat) return;
-  int64_t m = gt / per_mat;
-  int64_t rem = gt % per_mat;
-  int rb = (int)(rem / cg), c4 = (int)(rem % cg) * 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int ncg = (cols + 127) / 128, nrb = rows / 32;
+  if (unit >= mats * nrb * ncg) return;                          // whole waves leave together
+  const int64_t m = unit / ((int64_t)nrb * ncg);
+  const int rem = (int)(unit % ((int64_t)nrb * ncg));
+  const int rb = rem / ncg, c4 = (rem % ncg) * 128 + 4 * (lane & 31), h = lane >> 5;
+  const bool cok = c4 < cols;
   const float* base = x + (m * rows + (int64_t)rb * 32) * cols + c4;
+  float4 v[16];
   float4 amax = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int r = 0; r < 32; r++) {
-    float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
-    amax.x = fmaxf(amax.x, fabsf(v.x)); amax.y = fmaxf(amax.y, fabsf(v.y));
-    amax.z = fmaxf(amax.z, fabsf(v.z)); amax.w = fmaxf(amax.w, fabsf(v.w));
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const int r = 8 * (j >> 2) + 4 * h + (j & 3);
+    v[j] = cok ? *reinterpret_cast<const float4*>(base + (int64_t)r * cols) : make_float4(0.f, 0.f, 0.f, 0.f);
+    amax.x = fmaxf(amax.x, fabsf(v[j].x)); amax.y = fmaxf(amax.y, fabsf(v[j].y));
+    amax.z = fmaxf(amax.z, fabsf(v[j].z)); amax.w = fmaxf(amax.w, fabsf(v[j].w));
   }
+  amax.x = fmaxf(amax.x, __shfl_xor(amax.x, 32)); amax.y = fmaxf(amax.y, __shfl_xor(amax.y, 32));
+  amax.z = fmaxf(amax.z, __shfl_xor(amax.z, 32)); amax.w = fmaxf(amax.w, __shfl_xor(amax.w, 32));
+  if (!cok) return;
   const int lp = FMT == 0 ? 8 : 4;
-  uint32_t s0 = scale_code(amax.x, lp), s1 = scale_code(amax.y, lp), s2 = scale_code(amax.z, lp),
-           s3 = scale_code(amax.w, lp);
+  const uint32_t s0 = scale_code(amax.x, lp), s1 = scale_code(amax.y, lp), s2 = scale_code(amax.z, lp),
+                 s3 = scale_code(amax.w, lp);
+  if (h == 0)
+    *reinterpret_cast<uint32_t*>(scales + (m * nrb + rb) * cols + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
   if constexpr (FMT == 2) {
-    uint32_t pk[4][6] = {};
+    uint32_t pk[4][3] = {};
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
-      const uint32_t c[4] = {e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.x, 127 - (int)s0))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.y, 127 - (int)s1))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.z, 127 - (int)s2))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v.w, 127 - (int)s3)))};
+    for (int j = 0; j < 16; j++) {
+      const uint32_t c[4] = {e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].x, 127 - (int)s0))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].y, 127 - (int)s1))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].z, 127 - (int)s2))),
+                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].w, 127 - (int)s3)))};
+      // local field j: bits 6 j of the lane's 96
+      const int bit = 6 * j;
 #pragma unroll
-      for (int q = 0; q < 4; q++) pack6(pk[q], blk6_field(r), c[q]);
+      for (int q = 0; q < 4; q++) {
+        pk[q][bit / 32] |= c[q] << (bit % 32);
+        if (bit % 32 > 26) pk[q][bit / 32 + 1] |= c[q] >> (32 - bit % 32);
+      }
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      uint32_t* dst = reinterpret_cast<uint32_t*>(codes + ((m * (rows / 32) + rb) * cols + c4 + q) * 24);
-#pragma unroll
-      for (int w = 0; w < 6; w++) dst[w] = pk[q][w];
+      uint32_t* dst = reinterpret_cast<uint32_t*>(codes + ((m * nrb + rb) * cols + c4 + q) * 24 + 12 * h);
+      dst[0] = pk[q][0];
+      dst[1] = pk[q][1];
+      dst[2] = pk[q][2];
     }
-    *reinterpret_cast<uint32_t*>(scales + (m * (rows / 32) + rb) * cols + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
     return;
   }
   uint8_t* cbase = codes + (m * rows + (int64_t)rb * 32) * cols + c4;
-  for (int r = 0; r < 32; r++) {
-    float4 v = *reinterpret_cast<const float4*>(base + (int64_t)r * cols);
-    float y0 = __builtin_ldexpf(v.x, 127 - (int)s0), y1 = __builtin_ldexpf(v.y, 127 - (int)s1);
-    float y2 = __builtin_ldexpf(v.z, 127 - (int)s2), y3 = __builtin_ldexpf(v.w, 127 - (int)s3);
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const int r = 8 * (j >> 2) + 4 * h + (j & 3);
+    const float y0 = __builtin_ldexpf(v[j].x, 127 - (int)s0), y1 = __builtin_ldexpf(v[j].y, 127 - (int)s1);
+    const float y2 = __builtin_ldexpf(v[j].z, 127 - (int)s2), y3 = __builtin_ldexpf(v[j].w, 127 - (int)s3);
     uint32_t w;
     if constexpr (FMT == 0)
       w = e4m3_code4(y0, y1, y2, y3);
@@ -176,7 +194,6 @@ __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int r
           (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);
     *reinterpret_cast<uint32_t*>(cbase + (int64_t)r * cols) = w;
   }
-  *reinterpret_cast<uint32_t*>(scales + (m * (rows / 32) + rb) * cols + c4) = s0 | (s1 << 8) | (s2 << 16) | (s3 << 24);
 }
 
 extern "C" __global__ void __launch_bounds__(256) mxfa_quant_cols_e4m3(const float* x, int64_t mats, int rows, int cols,
