@@ -139,14 +139,20 @@ def time_calls(torch, fn, steps, warmup, preheat=True):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_hbm_traffic.txt")
-KERNEL_SOURCE = os.path.join(ROOT, "radiance-kernels_amd", "csrc", "mxfa_kernels.hip")
+# the device sources the code object is built from, hashed in this order
+KERNEL_SOURCES = [os.path.join(ROOT, "radiance-kernels_amd", "csrc", f)
+                  for f in ("mxfa_kernels.hip", "mx_device.h", "e3m2_rule.h", "mxfa_args.h", "log2_table.h")]
 
 
 def kernel_source_sha():
-    """sha256 (first 16 hex digits) of the kernel source the code object is built from."""
+    """sha256 (first 16 hex digits) of the device sources the code object is built from
+    (concatenated in KERNEL_SOURCES order)."""
     import hashlib
-    with open(KERNEL_SOURCE, "rb") as f:
-        return hashlib.sha256(f.read()).hexdigest()[:16]
+    h = hashlib.sha256()
+    for path in KERNEL_SOURCES:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def profile_fields(path, keys):

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "e3m2_rule.h"
 #include "log2_table.h"
 
 namespace mxfa {
@@ -129,41 +130,7 @@ __device__ __forceinline__ uint32_t r4_scale(float amax, float& mul) {
   return (uint32_t)(c < 0 ? 0 : (c > 254 ? 254 : c));
 }
 
-// lib/golden bf16 RNE (+-0 -> +0, tiny -> +0, NaN quieted).
-__device__ __forceinline__ uint32_t bf16_rne(float x) {
-  if (x == 0.0f) return 0u;
-  uint32_t b = __float_as_uint(x);
-  if (((b >> 23) & 0xffu) == 0xffu) {
-    uint32_t h = b >> 16;
-    if ((b & 0x7fffffu) && !(h & 0x40u)) h |= 0x40u;
-    return h & 0xffffu;
-  }
-  uint32_t r = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
-  return (r & 0x7fffu) == 0u ? 0u : r;
-}
 
-// R1 E3M2 code (6 bits, one per byte) of a bf16 pattern.
-__device__ __forceinline__ uint32_t e3m2_code_bf16(uint32_t h) {
-  uint32_t neg = (h >> 15) & 1u;
-  int E = (int)((h >> 7) & 0xffu), M = (int)(h & 0x7fu);
-  if (E == 0) return 0u;
-  uint32_t c;
-  if (E == 255) {
-    c = 0x1fu;                                   // inf / NaN -> E4M2 inf -> +-28
-  } else {
-    int e = E - 127;
-    if (e > 7 || e < -6) return 0u;              // reference maps both tails to 0
-    int q = M >> 5, r = (M >> 4) & 1, st = (M & 15) != 0;
-    int sig = q + (r & (st | (q & 1)));
-    if (sig == 4) { sig = 0; e++; }
-    if (e >= 5) c = 0x1fu;                       // >= 32 (or E4M2 overflow) -> 28
-    else if (e >= -2) c = ((uint32_t)(e + 3) << 2) | (uint32_t)sig;
-    else if (e == -3) c = sig < 2 ? 2u : 3u;     // 0.125 / 0.1875
-    else if (e == -4) c = sig < 2 ? 1u : 2u;     // 0.0625 / 0.125
-    else return 0u;                              // <= 0.0546875
-  }
-  return (neg << 5) | c;
-}
 
 // Element i (a 6-bit code) of a 32-element block packed little endian into six dwords: bits
 // 6i .. 6i + 5 of the 192 (i a compile-time constant after unrolling).

@@ -57,14 +57,15 @@ typedef __attribute__((address_space(3))) v2i lds_v2i;
 // ============================================================================
 // Quantizers (rule R1).  One MX block of 32 values is handled by 8 lanes.
 // ============================================================================
+// E4M3 codes of four values x 2^sh, or (FMT 1) E3M2 codes through the table e3m2_tab.
 template <int FMT>
-__device__ __forceinline__ uint32_t encode4(float4 v, int sh) {
+__device__ __forceinline__ uint32_t encode4(float4 v, int sh, const uint8_t* e3m2_tab = nullptr) {
   float y[4] = {__builtin_ldexpf(v.x, sh), __builtin_ldexpf(v.y, sh), __builtin_ldexpf(v.z, sh),
                 __builtin_ldexpf(v.w, sh)};
   if (FMT == 0) return e4m3_code4(y[0], y[1], y[2], y[3]);
   uint32_t w = 0;
 #pragma unroll
-  for (int i = 0; i < 4; i++) w |= e3m2_code_bf16(bf16_rne(y[i])) << (8 * i);
+  for (int i = 0; i < 4; i++) w |= e3m2_code_tab(y[i], e3m2_tab) << (8 * i);
   return w;
 }
 
@@ -72,6 +73,11 @@ __device__ __forceinline__ uint32_t encode4(float4 v, int sh) {
 template <int FMT>
 __device__ void quant_rows_impl(const float* __restrict__ x, int64_t nblocks, uint8_t* __restrict__ codes,
                                 uint8_t* __restrict__ scales) {
+  __shared__ uint8_t e3m2_tab[FMT == 0 ? 4 : E3M2_TAB_N];
+  if constexpr (FMT != 0) {
+    e3m2_tab_fill(e3m2_tab, threadIdx.x, blockDim.x);
+    __syncthreads();
+  }
   int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t blk = gt >> 3;
   int part = (int)(gt & 7);
@@ -82,7 +88,7 @@ __device__ void quant_rows_impl(const float* __restrict__ x, int64_t nblocks, ui
   a = fmaxf(a, __shfl_xor(a, 2));
   a = fmaxf(a, __shfl_xor(a, 4));
   uint32_t sc = scale_code(a, FMT == 0 ? 8 : 4);
-  reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = encode4<FMT>(v, 127 - (int)sc);
+  reinterpret_cast<uint32_t*>(codes)[blk * 8 + part] = encode4<FMT>(v, 127 - (int)sc, e3m2_tab);
   if (part == 0) scales[blk] = (uint8_t)sc;
 }
 
@@ -129,6 +135,11 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_quant_rows_r4(const float
 template <int FMT>
 __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int rows, int cols,
                                 uint8_t* __restrict__ codes, uint8_t* __restrict__ scales) {
+  __shared__ uint8_t e3m2_tab[FMT == 0 ? 4 : E3M2_TAB_N];
+  if constexpr (FMT != 0) {
+    e3m2_tab_fill(e3m2_tab, threadIdx.x, blockDim.x);
+    __syncthreads();
+  }
   const int lane = threadIdx.x & 63;
   const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int ncg = (cols + 127) / 128, nrb = rows / 32;
@@ -159,10 +170,10 @@ __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int r
     uint32_t pk[4][3] = {};
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-      const uint32_t c[4] = {e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].x, 127 - (int)s0))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].y, 127 - (int)s1))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].z, 127 - (int)s2))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(v[j].w, 127 - (int)s3)))};
+      const uint32_t c[4] = {e3m2_code_tab(__builtin_ldexpf(v[j].x, 127 - (int)s0), e3m2_tab),
+                             e3m2_code_tab(__builtin_ldexpf(v[j].y, 127 - (int)s1), e3m2_tab),
+                             e3m2_code_tab(__builtin_ldexpf(v[j].z, 127 - (int)s2), e3m2_tab),
+                             e3m2_code_tab(__builtin_ldexpf(v[j].w, 127 - (int)s3), e3m2_tab)};
       // local field j: bits 6 j of the lane's 96
       const int bit = 6 * j;
 #pragma unroll
@@ -190,8 +201,8 @@ __device__ void quant_cols_impl(const float* __restrict__ x, int64_t mats, int r
     if constexpr (FMT == 0)
       w = e4m3_code4(y0, y1, y2, y3);
     else
-      w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
-          (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);
+      w = e3m2_code_tab(y0, e3m2_tab) | (e3m2_code_tab(y1, e3m2_tab) << 8) | (e3m2_code_tab(y2, e3m2_tab) << 16) |
+          (e3m2_code_tab(y3, e3m2_tab) << 24);
     *reinterpret_cast<uint32_t*>(cbase + (int64_t)r * cols) = w;
   }
 }
@@ -247,7 +258,7 @@ __device__ __forceinline__ void kv_append_k_part(const float* k_new, int64_t gt,
 template <int FMT>
 __device__ __forceinline__ void kv_append_v_part(const float* v_new, float* v_tail, int64_t unit, int64_t nunits,
                                                  int lane, int ntouch, int n_new, int L, int D, int pos0,
-                                                 uint8_t* v_cache, uint8_t* v_sc) {
+                                                 uint8_t* v_cache, uint8_t* v_sc, const uint8_t* e3m2_tab) {
   if (unit >= nunits) return;                       // whole waves leave together
   const int upb = D / 32;
   const int64_t bk = unit / ((int64_t)ntouch * upb);
@@ -288,10 +299,10 @@ __device__ __forceinline__ void kv_append_v_part(const float* v_new, float* v_ta
     uint32_t pk[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t c[4] = {e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].x, 127 - (int)s0))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].y, 127 - (int)s1))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].z, 127 - (int)s2))),
-                             e3m2_code_bf16(bf16_rne(__builtin_ldexpf(x[i].w, 127 - (int)s3)))};
+      const uint32_t c[4] = {e3m2_code_tab(__builtin_ldexpf(x[i].x, 127 - (int)s0), e3m2_tab),
+                             e3m2_code_tab(__builtin_ldexpf(x[i].y, 127 - (int)s1), e3m2_tab),
+                             e3m2_code_tab(__builtin_ldexpf(x[i].z, 127 - (int)s2), e3m2_tab),
+                             e3m2_code_tab(__builtin_ldexpf(x[i].w, 127 - (int)s3), e3m2_tab)};
 #pragma unroll
       for (int q = 0; q < 4; q++) pk[q] |= c[q] << (6 * i);
       if (tail_here && p0 + 4 * rl + i >= pos0) *reinterpret_cast<float4*>(v_tail + (bk * 32 + 4 * rl + i) * D + c4) = x[i];
@@ -316,8 +327,8 @@ __device__ __forceinline__ void kv_append_v_part(const float* v_new, float* v_ta
     if constexpr (FMT == 0)
       w = e4m3_code4(y0, y1, y2, y3);
     else
-      w = e3m2_code_bf16(bf16_rne(y0)) | (e3m2_code_bf16(bf16_rne(y1)) << 8) |
-          (e3m2_code_bf16(bf16_rne(y2)) << 16) | (e3m2_code_bf16(bf16_rne(y3)) << 24);
+      w = e3m2_code_tab(y0, e3m2_tab) | (e3m2_code_tab(y1, e3m2_tab) << 8) | (e3m2_code_tab(y2, e3m2_tab) << 16) |
+          (e3m2_code_tab(y3, e3m2_tab) << 24);
     *reinterpret_cast<uint32_t*>(v_cache + (bk * L + p0 + r) * D + c4) = w;
     if (tail_here && p0 + r >= pos0) *reinterpret_cast<float4*>(v_tail + (bk * 32 + r) * D + c4) = x[i];
   }
@@ -333,8 +344,15 @@ __device__ void kv_append_impl(const float* k_new, const float* v_new, float* v_
     kv_append_k_part((const float*)k_new, (int64_t)blockIdx.x * blockDim.x + threadIdx.x, kblocks, n_new, L, D, pos0,
                      k_cache, k_sc);
   } else {
+    // (the workgroup's branch is uniform: the E3M2 table is filled by all its threads)
+    __shared__ uint8_t e3m2_tab[FMT == 0 ? 4 : E3M2_TAB_N];
+    if constexpr (FMT != 0) {
+      e3m2_tab_fill(e3m2_tab, threadIdx.x, blockDim.x);
+      __syncthreads();
+    }
     const int64_t unit = ((int64_t)blockIdx.x - kgroups) * (blockDim.x / 64) + (threadIdx.x >> 6);
-    kv_append_v_part<FMT>(v_new, v_tail, unit, vunits, threadIdx.x & 63, ntouch, n_new, L, D, pos0, v_cache, v_sc);
+    kv_append_v_part<FMT>(v_new, v_tail, unit, vunits, threadIdx.x & 63, ntouch, n_new, L, D, pos0, v_cache, v_sc,
+                          e3m2_tab);
   }
 }
 
