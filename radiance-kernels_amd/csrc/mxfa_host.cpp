@@ -243,25 +243,27 @@ const char* kernel_name(const char* kind, const mxfa_attn_params* p, bool v_suff
 
 // Split-KV plan: the 64-key blocks of each (b, KV head) are dealt to n_parts interleaved
 // partials (partial i: blocks i, i + n_parts, ...), one wave each, about kDecodeWaves
-// partial waves per call -- two per SIMD of the 256-CU chip.  At most 4 partials are
+// partial waves per call -- two per SIMD of the 256-CU chip, at the two workgroups per CU
+// of D <= 128; half as many at D = 256, whose kernel fits one workgroup per CU (measured
+// on B32 Hq16 Hkv8 L8192 D256: 0.169 ms at 1,024 waves, 0.182 at 2,048).  At most 4 partials are
 // rounded up to 1, 2 or 4 so that a head's partials fill whole 4-wave workgroups and merge
 // inside them.  Interleaving puts the partial waves of a head, which share a workgroup,
 // on adjacent blocks at the same time (measured on c5: 188 us vs 204 us for contiguous
 // chunks at 2048 waves).  MXFA_DECODE_WAVES overrides the target.
 constexpr int64_t kDecodeWaves = 2048;
 
-int64_t decode_wave_target() {
+int64_t decode_wave_target(int head_dim) {
   if (const char* env = getenv("MXFA_DECODE_WAVES")) {
     long long v = atoll(env);
     if (v > 0) return v;
   }
-  return kDecodeWaves;
+  return head_dim == 256 ? kDecodeWaves / 2 : kDecodeWaves;
 }
 
 int decode_parts(const mxfa_attn_params* p) {
   const int64_t bk = (int64_t)p->batch * p->num_kv_heads;
   const int64_t blocks = (p->seq_k + 63) / 64;
-  int64_t n = (decode_wave_target() + bk - 1) / bk;
+  int64_t n = (decode_wave_target(p->head_dim) + bk - 1) / bk;
   if (n == 3) n = 4;
   if (n > blocks) n = blocks;
   if (n < 1) n = 1;
@@ -668,12 +670,10 @@ mxfa_status decode_launch(DeviceModule* dm, const mxfa_attn_params* p, const uin
   int64_t nbh = (int64_t)p->batch * p->num_q_heads;
   a.part_o = reinterpret_cast<float*>(workspace);
   a.part_ml = a.part_o + nbh * nparts * p->head_dim;
-  // D <= 128: 4 waves per workgroup over the linear (b, KV head, chunk) items; D = 256:
-  // 2 waves (LDS-limited) over the chunks of one (b, KV head) per grid row
-  const int nw = p->head_dim == 256 ? 2 : 4;
+  // 4 waves per workgroup over the linear (b, KV head, chunk) items
+  const int nw = 4;
   const int64_t items = (int64_t)p->batch * p->num_kv_heads * nparts;
-  dim3 grid = p->head_dim == 256 ? dim3((unsigned)((nparts + nw - 1) / nw), (unsigned)(p->batch * p->num_kv_heads))
-                                 : dim3((unsigned)((items + nw - 1) / nw));
+  const dim3 grid((unsigned)((items + nw - 1) / nw));
   // When every head's partials fit in one workgroup (nparts divides its 4 waves) and the
   // valid columns' partials fit the waves' V slots (group <= 16), the kernel merges them
   // itself (same formula and order as mxfa_decode_combine) and no combine launch follows.
@@ -681,7 +681,7 @@ mxfa_status decode_launch(DeviceModule* dm, const mxfa_attn_params* p, const uin
   // bit-identical O; the switch exists to test exactly that).
   const char* comb = getenv("MXFA_DECODE_COMBINE");
   const bool force_kernel = comb && std::strcmp(comb, "kernel") == 0;
-  a.fuse_combine = !force_kernel && p->head_dim <= 128 && nw % nparts == 0 && a.group <= 16;
+  a.fuse_combine = !force_kernel && nw % nparts == 0 && a.group <= 16;
   void* args[] = {&a};
   if (mxfa_status st = launch(dm, kernel_name("decode", p, p->v_fmt == MXFA_FMT_E3M2_BLK), grid, dim3(64 * nw), args,
                               stream))

@@ -469,13 +469,11 @@ __device__ __forceinline__ v8i cat44(v4i lo, v4i hi) {
   return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// LDS tiles: K as bf16 (row pitch 2D + 16 bytes), V as fp8 codes (pitch D + 16);
-// the 16-byte pads keep row starts on distinct banks.
+// Decode LDS slots: a 64-key block of fp8 codes (K, then V) at row pitch D + 16 bytes,
+// whose 16-byte pad keeps row starts on distinct banks, and the block's V scales.
 template <int D> struct Lds {
   static constexpr int KP = D + 16;          // V row pitch (bytes)
-  static constexpr int KPB = 2 * D + 16;     // K (bf16) row pitch (bytes)
   static constexpr int TILE = BN * KP;
-  static constexpr int TILEK = BN * KPB;
   static constexpr int SC = BN * D / 32;
 };
 
@@ -615,23 +613,6 @@ extern "C" __global__ void __launch_bounds__(256) mxfa_softmax_requant_rows(
     softmax_requant_rows<P_R1>(s, row_max, c, rows, cols, p, codes, scales, row_sum);
 }
 
-// mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
-// S^T = K Q^T (bf16 MFMA) for one 64-key block from the LDS K tile: tile t covers keys
-// 32t .. 32t+31.
-template <int D>
-__device__ __forceinline__ void qk_tiles(v16f (&s)[BN / 32], const v4i* qb, const uint8_t* sKb, int lane) {
-  constexpr int KPB = Lds<D>::KPB;
-  const int r = lane & 31, h = lane >> 5;
-#pragma unroll
-  for (int t = 0; t < BN / 32; t++) {
-    s[t] = (v16f){};
-    const uint8_t* krow = sKb + (t * 32 + r) * KPB + 16 * h;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; kk++)
-      s[t] = mfma_bf16(*reinterpret_cast<const v4i*>(krow + 32 * kk), qb[kk], s[t]);
-  }
-}
-
 // Softmax, P requant and O^T += V^T P^T for one key block whose scores are in s.
 // mask: the block has keys outside [klo, khi] for some row of the wave (wave-uniform).
 // VBLK: the V tile is block-packed E3M2 as the caller stores it (two 32-key blocks of D
@@ -757,16 +738,6 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, v16f (&s)[BN / 32],
       st.o[dt] = mfma_mx(va, pb[kstep], st.o[dt], vscale, pscale);
     }
   }
-}
-
-// One key block for one wave: S^T tiles -> softmax -> requant P -> O^T += V^T P^T.
-template <int D, bool SOFTCAP, int PR, bool VBLK = false>
-__device__ __forceinline__ void wave_block(WaveState<D>& st, const v4i* qb, const uint8_t* sKb, const uint8_t* sV,
-                                           const uint8_t* sVs, int key0, int klo, int khi, bool mask,
-                                           const FaArgs& a, int lane) {
-  v16f s[BN / 32];
-  qk_tiles<D>(s, qb, sKb, lane);
-  softmax_pv<D, SOFTCAP, PR, VBLK>(st, s, sV, sVs, key0, klo, khi, mask, a, lane);
 }
 
 // Q operand (B of S^T = K Q^T, bf16) for query row `qrow` (zeros if invalid): MFMA kk
@@ -1699,14 +1670,14 @@ MXFA_PREFILL3_TRACE(256, true, P_R2, mxfa_prefill3_trace_d256_softcap_r2)
 // merged in part order (inside the workgroup, or by mxfa_decode_combine).  The group's
 // query heads are the wave's query columns (column c = head kvh*group + c).
 // ---------------------------------------------------------------------------
-// ---------------------------------------------------------------------------
-// Decode, D <= 128.  One wave per partial of one (b, KV head); its 32 score columns are
-// the group's query heads (columns >= group are padding).
+// One wave per partial of one (b, KV head); its 32 score columns are the group's query
+// heads (columns >= group are padding).
 // K and V are read in block order (whole lines per load instruction, non-temporal) and
 // pass through the wave's LDS slot in turn: K is read back in the split-d mapping and
 // dequantized to bf16 right before each score MFMA, then V takes the slot for the
 // ds_read_b64_tr_b8 reads of the PV step.  Small per-wave LDS and register footprints
-// give two workgroups per CU, whose waves hide each other's load latency.
+// give two workgroups per CU at D <= 128, whose waves hide each other's load latency; at
+// D = 256 one workgroup per CU keeps twice the bytes per wave in flight.
 // ---------------------------------------------------------------------------
 template <int D, bool SOFTCAP, int PR, bool VBLK = false>
 __device__ void decode_split_impl(const FaArgs& a) {
@@ -1716,10 +1687,16 @@ __device__ void decode_split_impl(const FaArgs& a) {
   constexpr int PERW = BN * CPR / 64;                 // K (and E4M3 V) chunks per lane
   constexpr int PERWV = VBLK ? 3 * D / 64 : PERW;     // V chunks per lane (block-packed: 48 D bytes)
   constexpr int SCW = BN * D / 32 / 4;                // V scale dwords per block
+  constexpr int SCPL = (SCW + 63) / 64;               // V scale dwords per lane
   constexpr int KC = D / 32;                          // 16-byte K chunks per lane per tile
+  constexpr int KSB = D / 64;                         // K scale bytes per half-row
   constexpr int KP = Lds<D>::KP;
   __shared__ __attribute__((aligned(16))) uint8_t sV[NW][Lds<D>::TILE];
   __shared__ __attribute__((aligned(16))) uint8_t sVs[NW][Lds<D>::SC];
+  // D = 256: the bf16 Q operand (64 registers) waits in LDS, MFMA kk's 64 lanes in one
+  // contiguous 1 KB row, so that a block's K and V codes stay in flight in registers
+  constexpr bool QLDS = D == 256;
+  __shared__ __attribute__((aligned(16))) v4i sQ[QLDS ? NW : 1][QLDS ? D / 16 * 64 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   // one (batch, KV head, chunk) item per wave, items numbered chunk-fastest over the
@@ -1738,8 +1715,15 @@ __device__ void decode_split_impl(const FaArgs& a) {
   const int64_t bh = (int64_t)b * a.Hq + head;
   const int qpos = a.q_pos0;                          // the single query's position
 
-  v4i qb[D / 16];
-  load_q_split<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
+  v4i qb[QLDS ? 1 : D / 16];
+  if constexpr (QLDS) {
+    v4i qt[D / 16];
+    load_q_split<D>(qt, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; kk++) sQ[wave][kk * 64 + lane] = qt[kk];
+  } else {
+    load_q_split<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
+  }
 
   // buffer resources end at Sk: rows past it read 0
   const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.k, (int64_t)bk * a.Skc * D, (int64_t)a.Sk * D);
@@ -1780,20 +1764,26 @@ __device__ void decode_split_impl(const FaArgs& a) {
   // LDS slot before the scores) and the E8M0 scales of this lane's K half-rows (keys
   // key0 + 32t + r).  A disabled load gets an offset past every resource: it reads nothing
   // and returns 0; no branch, so the waits on the other loads stay partial.
+  // KH: the block's K loads go out in KH parts (part u: tiles NT/KH u ..), each just before
+  // the scores that free its registers' previous contents -- at D = 256 the second tile's
+  // loads wait for the first tile's scores, which keeps the peak register demand in bounds
+  constexpr int KH = QLDS ? 2 : 1;
   v4i kr[PERW];
   uint32_t ksr[NT];
-  auto load_k = [&](int key0, bool on) {
+  auto load_k = [&](int key0, bool on, int u) {
 #pragma unroll
-    for (int i = 0; i < PERW; i++) {
+    for (int i = u * (PERW / KH); i < (u + 1) * (PERW / KH); i++) {
       const int c = lane + 64 * i;
       const uint32_t ko = on ? (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16) : 0x80000000u;
       kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, kNonTemporal);
     }
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
+    for (int t = u * (NT / KH); t < (u + 1) * (NT / KH); t++) {
       const int row = key0 + 32 * t + r;
-      const uint32_t so = on ? (uint32_t)(D == 128 ? row * 4 + 2 * h : row * 2 + h) : 0x80000000u;
-      if constexpr (D == 128)
+      const uint32_t so = on ? (uint32_t)(row * (D / 32) + KSB * h) : 0x80000000u;
+      if constexpr (KSB == 4)
+        ksr[t] = __builtin_amdgcn_raw_buffer_load_b32(rks, so, 0, 0);
+      else if constexpr (KSB == 2)
         ksr[t] = __builtin_amdgcn_raw_buffer_load_b16(rks, so, 0, 0);
       else
         ksr[t] = __builtin_amdgcn_raw_buffer_load_b8(rks, so, 0, 0);
@@ -1802,7 +1792,7 @@ __device__ void decode_split_impl(const FaArgs& a) {
   // V codes and scales of a block (stored to the wave's LDS slot after its scores); block-
   // packed V: the block's 48 D contiguous bytes, chunk c at byte 16 c of the slot
   v4i vr[PERWV];
-  uint32_t vsr;
+  uint32_t vsr[SCPL];
   auto load_v = [&](int key0, bool on) {
 #pragma unroll
     for (int i = 0; i < PERWV; i++) {
@@ -1812,12 +1802,17 @@ __device__ void decode_split_impl(const FaArgs& a) {
                                  : (uint32_t)((key0 + c / CPR) * D + (c % CPR) * 16);
       vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kNonTemporal);
     }
-    const uint32_t so = on && lane < SCW ? (uint32_t)((key0 / 32) * D + 4 * lane) : 0x80000000u;
-    vsr = __builtin_amdgcn_raw_buffer_load_b32(rvs, so, 0, kNonTemporal);
+#pragma unroll
+    for (int i = 0; i < SCPL; i++) {
+      const int d = lane + 64 * i;
+      const uint32_t so = on && d < SCW ? (uint32_t)((key0 / 32) * D + 4 * d) : 0x80000000u;
+      vsr[i] = __builtin_amdgcn_raw_buffer_load_b32(rvs, so, 0, kNonTemporal);
+    }
   };
   // one block ahead: K(j+1) goes out once K(j) is in LDS, V(j+1) once V(j) is, and both
   // stay in flight through the scores, softmax and PV of block j
-  load_k(kfirst, kfirst < klast);
+#pragma unroll
+  for (int u = 0; u < KH; u++) load_k(kfirst, kfirst < klast, u);
   load_v(kfirst, kfirst < klast);
   for (int key0 = kfirst; key0 < klast; key0 += kstride) {
     // K tile into the wave's slot (row pitch KP, like V), then each lane reads back its
@@ -1830,27 +1825,34 @@ __device__ void decode_split_impl(const FaArgs& a) {
       const int c = lane + 64 * i;
       *reinterpret_cast<v4i*>(&sV[wave][(c / CPR) * KP + (c % CPR) * 16]) = kr[i];
     }
-    // the next block's K goes out as soon as this block's codes are in LDS (its scales
-    // replace this block's, which the scores still need: they are kept in ksc)
+    // the next block's K goes out once this block's codes are in LDS (at D = 256 half of it
+    // waits for the first tile's scores); its scales replace this block's, which the
+    // scores still need: they are kept in ksc
     uint32_t ksc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) ksc[t] = ksr[t];
-    load_k(key0 + kstride, key0 + kstride < klast);
     // scores: K dequantized to bf16 just before each MFMA
     v16f sc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      v4i kt[KC];
-#pragma unroll
-      for (int c = 0; c < KC; c++)
-        kt[c] = *reinterpret_cast<const v4i*>(&sV[wave][(32 * t + r) * KP + h * (D / 2) + 16 * c]);
+      if (t % (NT / KH) == 0) load_k(key0 + kstride, key0 + kstride < klast, t / (NT / KH));
+      // K half-row chunks read from LDS KR at a time (D = 256: half the row per read group)
+      constexpr int KR = QLDS ? KC / 2 : KC;
       sc[t] = (v16f){};
 #pragma unroll
-      for (int kk = 0; kk < D / 16; kk++) {
-        const v4i& w = kt[kk / 2];
-        const float scale = e8m0_as_float((ksc[t] >> (8 * (kk / 4))) & 0xffu);
-        const v4i ka = fp8x8_to_bf16x8((uint32_t)w[2 * (kk & 1)], (uint32_t)w[2 * (kk & 1) + 1], scale);
-        sc[t] = mfma_bf16(ka, qb[kk], sc[t]);
+      for (int c0 = 0; c0 < KC; c0 += KR) {
+        v4i kt[KR];
+#pragma unroll
+        for (int c = 0; c < KR; c++)
+          kt[c] = *reinterpret_cast<const v4i*>(&sV[wave][(32 * t + r) * KP + h * (D / 2) + 16 * (c0 + c)]);
+#pragma unroll
+        for (int k2 = 0; k2 < 2 * KR; k2++) {
+          const int kk = 2 * c0 + k2;
+          const v4i& w = kt[k2 / 2];
+          const float scale = e8m0_as_float((ksc[t] >> (8 * (kk / 4))) & 0xffu);
+          const v4i ka = fp8x8_to_bf16x8((uint32_t)w[2 * (kk & 1)], (uint32_t)w[2 * (kk & 1) + 1], scale);
+          sc[t] = mfma_bf16(ka, QLDS ? sQ[wave][kk * 64 + lane] : qb[kk], sc[t]);
+        }
       }
     }
     __asm__ volatile("" ::: "memory");
@@ -1864,7 +1866,9 @@ __device__ void decode_split_impl(const FaArgs& a) {
       }
       *reinterpret_cast<v4i*>(&sV[wave][VBLK ? 16 * c : (c / CPR) * KP + (c % CPR) * 16]) = zv;
     }
-    if (lane < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * lane]) = vsr;
+#pragma unroll
+    for (int i = 0; i < SCPL; i++)
+      if (lane + 64 * i < SCW) *reinterpret_cast<uint32_t*>(&sVs[wave][4 * (lane + 64 * i)]) = vsr[i];
     load_v(key0 + kstride, key0 + kstride < klast);
     // LDS operations of one wave complete in order: the V tile written above is in place
     // for the transposed reads, and the next block's writes follow this block's reads
@@ -1954,118 +1958,6 @@ __device__ void decode_split_impl(const FaArgs& a) {
   }
 }
 
-// Waves per decode workgroup (each wave has private LDS tiles).
-template <int D> struct DecodeWaves { static constexpr int N = D == 256 ? 2 : 4; };
-
-template <int D, bool SOFTCAP, int PR, bool VBLK = false>
-__device__ void decode_impl(const FaArgs& a) {
-  constexpr int NW = DecodeWaves<D>::N;
-  __shared__ __attribute__((aligned(16))) uint8_t sK[NW][Lds<D>::TILEK];
-  __shared__ __attribute__((aligned(16))) uint8_t sV[NW][Lds<D>::TILE];
-  __shared__ __attribute__((aligned(16))) uint8_t sVs[NW][Lds<D>::SC];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 31, h = lane >> 5;
-  const int part = blockIdx.x * NW + wave;
-  const int bk = blockIdx.y;
-  if (part >= a.n_qblk) return;                       // waves past the last chunk have no work
-  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
-  const bool qvalid = r < a.group;
-  const int head = kvh * a.group + (qvalid ? r : 0);
-  const int64_t bh = (int64_t)b * a.Hq + head;
-  const int qpos = a.q_pos0;                          // the single query's position
-
-  v4i qb[D / 16];
-  load_q<D>(qb, a.q + bh * D, a.qs + bh * (D / 32), qvalid, h);
-
-  const uint8_t* kb = a.k + (int64_t)bk * a.Skc * D;
-  const uint8_t* ksb = a.ks + (int64_t)bk * a.Skc * (D / 32);
-  const uint8_t* vb = a.v + (int64_t)bk * (VBLK ? (a.Skc / 32) * (24 * D) : (int64_t)a.Skc * D);
-  const uint8_t* vsb = a.vs + (int64_t)bk * (a.Skc / 32) * D;
-
-  // partial `part` of n_qblk takes the key blocks part, part + n_qblk, ...
-  const int kend = a.Sk;
-  int klo, khi;
-  key_limits(a, qpos, qvalid, klo, khi);
-
-  WaveState<D> st;
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) st.o[dt] = (v16f){};
-  st.m = -INFINITY;
-  st.l = 0.0f;
-
-  // each wave stages its own blocks through its own LDS slot (64 lanes load)
-  constexpr int CPR = D / 16;
-  constexpr int PERW = BN * CPR / 64;
-  constexpr int KP = Lds<D>::KP;
-  constexpr int KPB = Lds<D>::KPB;
-  for (int key0 = part * BN; key0 < kend; key0 += a.n_qblk * BN) {
-#pragma unroll
-    for (int i = 0; i < PERW; i++) {
-      int c = lane + 64 * i;
-      int row = c / CPR, col = (c % CPR) * 16;
-      int key = key0 + row;
-      v4i zk = {0, 0, 0, 0}, zv = {0, 0, 0, 0};
-      uint32_t ksc = 0;
-      if (key < kend) {
-        zk = *reinterpret_cast<const v4i*>(kb + (int64_t)key * D + col);
-        if (!VBLK) zv = *reinterpret_cast<const v4i*>(vb + (int64_t)key * D + col);
-        ksc = ksb[(int64_t)key * (D / 32) + col / 32];
-      }
-      if (!VBLK && a.v_e3m2) {
-#pragma unroll
-        for (int w = 0; w < 4; w++) zv[w] = (int)e3m2x4_to_e4m3x4((uint32_t)zv[w]);
-      }
-      float sc = e8m0_as_float(ksc);
-      v4i b0 = fp8x8_to_bf16x8((uint32_t)zk[0], (uint32_t)zk[1], sc);
-      v4i b1 = fp8x8_to_bf16x8((uint32_t)zk[2], (uint32_t)zk[3], sc);
-      *reinterpret_cast<v4i*>(&sK[wave][row * KPB + col * 2]) = b0;
-      *reinterpret_cast<v4i*>(&sK[wave][row * KPB + col * 2 + 16]) = b1;
-      if (!VBLK) *reinterpret_cast<v4i*>(&sV[wave][row * KP + col]) = zv;
-    }
-    if constexpr (VBLK) {
-      // the block's 48 D bytes as they are (a 32-key block past Sk reads 0)
-#pragma unroll
-      for (int i = 0; i < 3 * D / 64; i++) {
-        const int c = lane + 64 * i;
-        const int kb32 = 16 * c / (24 * D);
-        v4i zv = {0, 0, 0, 0};
-        if (key0 + 32 * kb32 < kend)
-          zv = *reinterpret_cast<const v4i*>(vb + (int64_t)(key0 / 32) * (24 * D) + 16 * c);
-        *reinterpret_cast<v4i*>(&sV[wave][16 * c]) = zv;
-      }
-    }
-    constexpr int SCW = BN * D / 32 / 4;   // V scale dwords per block
-    for (int i = lane; i < SCW; i += 64) {
-      int byte = i * 4;
-      int vk32 = key0 / 32 + byte / D;
-      uint32_t vw = vk32 * 32 < kend ? *reinterpret_cast<const uint32_t*>(vsb + (int64_t)(key0 / 32) * D + byte) : 0u;
-      *reinterpret_cast<uint32_t*>(&sVs[wave][byte]) = vw;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    // columns >= group are padding and must be masked
-    wave_block<D, SOFTCAP, PR, VBLK>(st, qb, sK[wave], sV[wave], sVs[wave], key0, klo, khi, true, a, lane);
-    __builtin_amdgcn_wave_barrier();
-  }
-
-  // partial outputs (unnormalized O, m in x units, full l)
-  float l = pair_sum(st.l);
-  const int nparts = a.n_qblk;
-  if (qvalid) {
-    float* po = a.part_o + (bh * nparts + part) * D;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-      for (int g = 0; g < 4; g++)
-        *reinterpret_cast<float4*>(po + dt * 32 + 8 * g + 4 * h) =
-            make_float4(st.o[dt][4 * g], st.o[dt][4 * g + 1], st.o[dt][4 * g + 2], st.o[dt][4 * g + 3]);
-    if (h == 0) {
-      a.part_ml[(bh * nparts + part) * 2] = st.m;
-      a.part_ml[(bh * nparts + part) * 2 + 1] = l;
-    }
-  }
-}
-
 // Decode partials of mxfa_decode_noalloc: one array per device, in this code object, so that
 // callers that cannot allocate (graph capture, serving loops) need no workspace.  The host
 // takes its device address from the loaded module (hipModuleGetGlobal) once per device and
@@ -2074,40 +1966,25 @@ __device__ void decode_impl(const FaArgs& a) {
 // that overlap on one device share (and race on) the array.
 __device__ __attribute__((used, aligned(256))) uint8_t mxfa_decode_scratch[MXFA_DECODE_SCRATCH_BYTES];
 
-#define MXFA_DECODE_SPLIT(D, SC, PR, NAME)                                             \
-  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC, PR>(a); }
-#define MXFA_DECODE(D, SC, PR, NAME)                                                   \
-  extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<D>::N) NAME(FaArgs a) { decode_impl<D, SC, PR>(a); }
-MXFA_DECODE_SPLIT(64, false, P_R1, mxfa_decode_d64)
-MXFA_DECODE_SPLIT(128, false, P_R1, mxfa_decode_d128)
-MXFA_DECODE(256, false, P_R1, mxfa_decode_d256)
-MXFA_DECODE_SPLIT(64, true, P_R1, mxfa_decode_d64_softcap)
-MXFA_DECODE_SPLIT(128, true, P_R1, mxfa_decode_d128_softcap)
-MXFA_DECODE(256, true, P_R1, mxfa_decode_d256_softcap)
-MXFA_DECODE_SPLIT(64, false, P_R2, mxfa_decode_d64_r2)
-MXFA_DECODE_SPLIT(128, false, P_R2, mxfa_decode_d128_r2)
-MXFA_DECODE(256, false, P_R2, mxfa_decode_d256_r2)
-MXFA_DECODE_SPLIT(64, true, P_R2, mxfa_decode_d64_softcap_r2)
-MXFA_DECODE_SPLIT(128, true, P_R2, mxfa_decode_d128_softcap_r2)
-MXFA_DECODE(256, true, P_R2, mxfa_decode_d256_softcap_r2)
-// block-packed E3M2 V (read as the fp6 operand)
-#define MXFA_DECODE_BLK(D, SC, PR, NAME)                                                \
-  extern "C" __global__ void __launch_bounds__(256, 2) NAME(FaArgs a) { decode_split_impl<D, SC, PR, true>(a); }
-#define MXFA_DECODE256_BLK(SC, PR, NAME)                                                \
-  extern "C" __global__ void __launch_bounds__(64 * DecodeWaves<256>::N) NAME(FaArgs a) { \
-    decode_impl<256, SC, PR, true>(a);                                                  \
+// D = 256 holds its O accumulators, Q fragments and a block of K and V codes in flight in
+// about 400 registers: one workgroup (one wave per SIMD) per CU.
+#define MXFA_DECODE_SPLIT(D, SC, PR, VBLK, NAME)                                                   \
+  extern "C" __global__ void __launch_bounds__(256, D == 256 ? 1 : 2) NAME(FaArgs a) {             \
+    decode_split_impl<D, SC, PR, VBLK>(a);                                                         \
   }
-#define MXFA_DECODE_BLK_ALL(D)                                                 \
-  MXFA_DECODE_BLK(D, false, P_R1, mxfa_decode_d##D##_blk)                     \
-  MXFA_DECODE_BLK(D, true, P_R1, mxfa_decode_d##D##_softcap_blk)              \
-  MXFA_DECODE_BLK(D, false, P_R2, mxfa_decode_d##D##_r2_blk)                  \
-  MXFA_DECODE_BLK(D, true, P_R2, mxfa_decode_d##D##_softcap_r2_blk)
-MXFA_DECODE_BLK_ALL(64)
-MXFA_DECODE_BLK_ALL(128)
-MXFA_DECODE256_BLK(false, P_R1, mxfa_decode_d256_blk)
-MXFA_DECODE256_BLK(true, P_R1, mxfa_decode_d256_softcap_blk)
-MXFA_DECODE256_BLK(false, P_R2, mxfa_decode_d256_r2_blk)
-MXFA_DECODE256_BLK(true, P_R2, mxfa_decode_d256_softcap_r2_blk)
+#define MXFA_DECODE_ALL(D)                                                                          \
+  MXFA_DECODE_SPLIT(D, false, P_R1, false, mxfa_decode_d##D)                                       \
+  MXFA_DECODE_SPLIT(D, true, P_R1, false, mxfa_decode_d##D##_softcap)                              \
+  MXFA_DECODE_SPLIT(D, false, P_R2, false, mxfa_decode_d##D##_r2)                                  \
+  MXFA_DECODE_SPLIT(D, true, P_R2, false, mxfa_decode_d##D##_softcap_r2)                           \
+  /* block-packed E3M2 V (read as the fp6 operand) */                                              \
+  MXFA_DECODE_SPLIT(D, false, P_R1, true, mxfa_decode_d##D##_blk)                                  \
+  MXFA_DECODE_SPLIT(D, true, P_R1, true, mxfa_decode_d##D##_softcap_blk)                           \
+  MXFA_DECODE_SPLIT(D, false, P_R2, true, mxfa_decode_d##D##_r2_blk)                               \
+  MXFA_DECODE_SPLIT(D, true, P_R2, true, mxfa_decode_d##D##_softcap_r2_blk)
+MXFA_DECODE_ALL(64)
+MXFA_DECODE_ALL(128)
+MXFA_DECODE_ALL(256)
 
 // Merge nparts partials per (b, query head) in part order: O = sum_i O_i 2^{(m_i - M) c} / sum_i l_i 2^{(m_i - M) c}.
 // One workgroup of D threads per query head.

@@ -188,6 +188,10 @@ def test_decode_config5_sampled():
     (3, 8, 2, 480, 64, 18, 0, 30.0),          # 3 -> 4 partials, ragged last block, softcap, D = 64
     (2, 64, 4, 1056, 128, 16, 0, 0.0),        # group 16, ragged last block
     (4, 32, 8, 1024, 128, 256, 0, 0.0),       # 8 partials: not fused, both runs use the kernel
+    (2, 16, 8, 1024, 256, 32, 0, 50.0),       # D = 256 (one workgroup per CU): 2 partials, softcap
+    (2, 16, 8, 1056, 256, 64, 200, 0.0),      # D = 256: 4 partials, window, ragged last block
+    (1, 32, 2, 512, 256, 4, 0, 0.0),          # D = 256, group 16: merge slots full
+    (2, 16, 4, 2048, 256, 128, 0, 0.0),       # D = 256: 16 partials through the kernel
 ])
 def test_decode_fused_merge_matches_combine_kernel(monkeypatch, B, Hq, Hkv, L, D, waves, window, softcap):
     """The in-workgroup merge of the interleaved partials (one launch) and
