@@ -249,6 +249,36 @@ def calibrate_copy(torch):
     print(json.dumps({"calibration": "device copy", "bytes_per_copy": n, "copies": 3}), flush=True)
 
 
+def bench_decode_d256(torch, mxfa, args):
+    """Decode at configs[3]'s head shape (Gemma-like: Hq 16, Hkv 8, D 256, softcap 50) over a
+    batch of 32 caches of 8,192 tokens, V as E4M3 and as block-packed E3M2.  Bytes = codes and
+    scales of Q, K, V read + fp32 O written."""
+    dev = "cuda:0"
+    B, Hq, Hkv, L, D = 32, 16, 8, 8192, 256
+    Q = torch.empty((B, Hq, 1, D), dtype=torch.float32, device=dev)
+    X = torch.empty((B, Hkv, L, D), dtype=torch.float32, device=dev)
+    mxfa.fill_normal(Q, 21)
+    mxfa.fill_normal(X, 22)
+    q, qs = mxfa.quantize_rows(Q)
+    k, ks = mxfa.quantize_rows(X)
+    mxfa.fill_normal(X, 23)
+    vs_ = {fmt: mxfa.quantize_cols(X, fmt) for fmt in (mxfa.FMT_E4M3, mxfa.FMT_E3M2_BLK)}
+    del X
+    o = torch.empty((B, Hq, 1, D), dtype=torch.float32, device=dev)
+    out = {"workload": f"decode B={B} Hq={Hq} Hkv={Hkv} D={D} KV length {L}, softcap 50"}
+    for key, fmt in (("v_e4m3", mxfa.FMT_E4M3), ("v_e3m2_blk", mxfa.FMT_E3M2_BLK)):
+        v, vsc = vs_[fmt]
+        p = mxfa.make_params(B, Hq, Hkv, 1, L, D, causal=True, q_pos0=L - 1, softcap=50.0, v_fmt=fmt)
+        _, wsb = mxfa.decode_plan(p)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        ms = time_calls(torch, lambda: mxfa.decode(p, q, qs, k, ks, v, vsc, out=o, workspace=ws),
+                        args.steps * 5, args.warmup)
+        nb = sum(t.numel() for t in (q, qs, k, ks, v, vsc)) + o.numel() * 4
+        out[key] = {"ms_per_call": round(ms, 4), "bytes_per_call": nb, "value": round(nb / (ms * 1e-3) / 1e9, 1),
+                    "unit": "GB/s"}
+    return out
+
+
 def bench_kv_append(torch, mxfa, args):
     """KV-cache append (mxfa_kv_append): a 4096-token prefill chunk into a configs[2]-shape
     cache (B=2, Hkv=8, D=128) and a one-token decode step into a configs[4]-shape cache
@@ -397,8 +427,10 @@ def profile_workload(torch, mxfa, name, args):
             p.p_rule = mxfa.P_R2
     elif name in OTHER_CONFIGS:
         p, ops = make_prefill(torch, mxfa, OTHER_CONFIGS[name], seed=7)
-    elif name == "decode":
-        dc = decode_config()
+    elif name in ("decode", "decode256"):
+        # decode256: bench_decode_d256's shape (Hq 16, Hkv 8, D 256, softcap 50, B 32, L 8192)
+        dc = decode_config() if name == "decode" else dict(B=32, Hq=16, Hkv=8, L=8192, D=256)
+        cap = 0.0 if name == "decode" else 50.0
         Qd = torch.empty((dc["B"], dc["Hq"], 1, dc["D"]), dtype=torch.float32, device=dev)
         Kd = torch.empty((dc["B"], dc["Hkv"], dc["L"], dc["D"]), dtype=torch.float32, device=dev)
         mxfa.fill_normal(Qd, 11)
@@ -408,7 +440,8 @@ def profile_workload(torch, mxfa, name, args):
         mxfa.fill_normal(Kd, 13)
         vd, vsd = mxfa.quantize_cols(Kd)
         del Kd
-        pd = mxfa.make_params(dc["B"], dc["Hq"], dc["Hkv"], 1, dc["L"], dc["D"], causal=True, q_pos0=dc["L"] - 1)
+        pd = mxfa.make_params(dc["B"], dc["Hq"], dc["Hkv"], 1, dc["L"], dc["D"], causal=True, q_pos0=dc["L"] - 1,
+                              softcap=cap)
         _, ws_bytes = mxfa.decode_plan(pd)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         od = torch.empty((dc["B"], dc["Hq"], 1, dc["D"]), dtype=torch.float32, device=dev)
@@ -451,7 +484,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="only run a 256 MiB device copy x3")
     ap.add_argument("--profile", metavar="WORKLOAD",
-                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode, gemm): W untimed + K timed calls")
+                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode, decode256, gemm): W untimed + K timed calls")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus must be 1 (the path is not sharded across GPUs here)",
@@ -558,6 +591,7 @@ def main():
 
     if not args.no_decode:
         result["decode"]["hbm_copy_gbs"] = hbm_copy_gbs(torch)
+        result["decode"]["d256"] = bench_decode_d256(torch, mxfa, args)
         result["kv_append"] = bench_kv_append(torch, mxfa, args)
         result["gemm"] = bench_gemm(torch, mxfa, args)
         result["other_configs"] = bench_other_configs(torch, mxfa, args)
