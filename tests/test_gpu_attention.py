@@ -181,6 +181,16 @@ def test_decode_config5_sampled():
     assert torch.equal(out, out2)
 
 
+def test_decode_d256_full_shape_sampled():
+    """Decode at D = 256 over 32 caches of 8,192 tokens (Gemma heads: Hq 16, Hkv 8, softcap
+    50; the shape bench.py times), sampled heads against the oracle; a second call gives the
+    same O bit for bit."""
+    p, dev, out = run_decode(32, 16, 8, 8192, 256, seed=37, heads=[0, 255, 511], softcap=50.0)
+    out2 = mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,L,D,waves,window,softcap", [
     (4, 32, 8, 1024, 128, 32, 0, 0.0),        # 1 partial per head
     (4, 32, 8, 1024, 128, 64, 0, 0.0),        # 2 partials

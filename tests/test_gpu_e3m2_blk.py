@@ -166,9 +166,8 @@ def test_kv_append_blk_matches_one_shot_then_prefill():
     (1, 8, 8, 800, 256, 0.0, mxfa.P_R2, 0),
 ])
 def test_decode_blk_matches_oracle_and_byte_e3m2(B, Hq, Hkv, L, D, softcap, p_rule, window):
-    """Decode over block-packed E3M2 V: the D <= 128 kernel loads each block's 48 D bytes
-    into the wave's LDS slot, the D = 256 kernel per 32-key block up to the sequence end; PV
-    reads them as the fp6 operand.  Against the oracle (codes unpacked) and the byte-E3M2
+    """Decode over block-packed E3M2 V: each 64-key block's 48 D bytes go unchanged into the
+    wave's LDS slot (loads past seq_k / 32 blocks read 0); PV reads them as the fp6 operand.  Against the oracle (codes unpacked) and the byte-E3M2
     decode (same values: O within a few ulps)."""
     print(f"blk decode B{B} Hq{Hq} Hkv{Hkv} L{L} D{D} softcap {softcap} p_rule {p_rule} window {window}", flush=True)
     L32 = -(-L // 32) * 32
