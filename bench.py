@@ -141,7 +141,8 @@ def time_calls(torch, fn, steps, warmup, preheat=True):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_c3_hbm_traffic.txt")
 # the device sources the code object is built from, hashed in this order
 KERNEL_SOURCES = [os.path.join(ROOT, "radiance-kernels_amd", "csrc", f)
-                  for f in ("mxfa_kernels.hip", "mx_device.h", "e3m2_rule.h", "mxfa_args.h", "log2_table.h")]
+                  for f in ("mxfa_kernels.hip", "kernel_base.h", "k_quant.hip", "k_attn_common.hip", "k_prefill.hip",
+                            "k_decode.hip", "k_gemm.hip", "mx_device.h", "e3m2_rule.h", "mxfa_args.h", "log2_table.h")]
 
 
 def kernel_source_sha():
