@@ -9,7 +9,7 @@ torch = pytest.importorskip("torch")
 
 import mxfa  # noqa: E402
 import oracle as O  # noqa: E402
-from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, gen_qkv, np_, oracle_params  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, explain_max_abs, gen_qkv, np_, oracle_params  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -50,7 +50,11 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
         want = want.reshape(B * Hq, Sq, D)[idx]
     rel, mab = errors(o, want)
     print(f"   rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
-    assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL
+    assert rel <= REL_L2_TOL
+    if mab > MAX_ABS_TOL:
+        # only where P code boundaries hit between fp32 and double P account for every excess
+        assert heads is None, "max-abs bound exceeded"
+        explain_max_abs(p, dev, host, o, want)
     if not same_kernel_order:
         o2 = np_(out_nw)
         assert np.all(np.isfinite(o2))
@@ -58,7 +62,10 @@ def run_case(B, Hq, Hkv, Sq, Sk, D, causal=False, q_pos0=0, window=0, softcap=0.
             o2 = o2.reshape(B * Hq, Sq, D)[idx]
         rel2, mab2 = errors(o2, want)
         print(f"   workspace-free kernel: rel-L2 {rel2:.3e} max-abs {mab2:.3e}", flush=True)
-        assert rel2 <= REL_L2_TOL and mab2 <= MAX_ABS_TOL
+        assert rel2 <= REL_L2_TOL
+        if mab2 > MAX_ABS_TOL:
+            assert heads is None, "max-abs bound exceeded"
+            explain_max_abs(p, dev, host, o2, want)
     return p, dev, out
 
 
@@ -113,25 +120,24 @@ def test_deterministic():
 
 
 @pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
-def test_baseline_configs_sampled_heads(cfg):
-    """Full BASELINE shapes; all heads computed on the GPU (coverage + finiteness),
-    a sample of heads compared with the oracle."""
+def test_baseline_configs_all_heads(cfg):
+    """Full BASELINE shapes, every head against the oracle (the threaded C oracle takes a
+    few seconds per configuration)."""
     if cfg == "c2":
-        run_case(4, 16, 16, 2048, 2048, 128, causal=True, seed=21, heads=[0, 11, 26, 37, 48, 63], check_codes=False)
+        run_case(4, 16, 16, 2048, 2048, 128, causal=True, seed=21, check_codes=False)
     elif cfg == "c3":
-        run_case(2, 32, 8, 4096, 4096, 128, causal=True, outlier_p=0.01, seed=22, heads=[0, 5, 18, 31, 44, 63],
-                 check_codes=False)
+        run_case(2, 32, 8, 4096, 4096, 128, causal=True, outlier_p=0.01, seed=22, check_codes=False)
     else:
         run_case(1, 16, 8, 8192, 8192, 256, causal=True, window=4096, softcap=50.0, v_fmt=mxfa.FMT_E3M2, seed=23,
-                 heads=[0, 3, 14], check_codes=False)
+                 check_codes=False)
 
 
 def test_softcap_stress_config4_shape():
     """The reference's softcap stress (Q x 50, kernels/flash_attention_mx_gemma/fa_gen_data.py:
     77-79,98) at the Gemma config's full shape: B=1 Hq=16 Hkv=8 S=8192 D=256, window 4096,
-    softcap 50, E3M2 V; sampled heads against the oracle."""
+    softcap 50, E3M2 V; every head against the oracle."""
     run_case(1, 16, 8, 8192, 8192, 256, causal=True, window=4096, softcap=50.0, v_fmt=mxfa.FMT_E3M2, seed=24,
-             q_mul=50.0, heads=[6], check_codes=False)
+             q_mul=50.0, check_codes=False)
 
 
 def run_decode(B, Hq, Hkv, L, D, seed, heads=None, v_fmt=mxfa.FMT_E4M3, softcap=0.0, p_rule=mxfa.P_R1):
@@ -173,19 +179,19 @@ def test_decode_ragged_and_e3m2():
     run_decode(2, 16, 8, 2080, 256, seed=32, softcap=30.0)
 
 
-def test_decode_config5_sampled():
+def test_decode_config5_all_heads():
     """B=64, Hq=32, Hkv=8, D=128, KV length 8192."""
-    p, dev, out = run_decode(64, 32, 8, 8192, 128, seed=33, heads=[0, 1000, 2047])
+    p, dev, out = run_decode(64, 32, 8, 8192, 128, seed=33)
     out2 = mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
 
 
-def test_decode_d256_full_shape_sampled():
+def test_decode_d256_full_shape():
     """Decode at D = 256 over 32 caches of 8,192 tokens (Gemma heads: Hq 16, Hkv 8, softcap
-    50; the shape bench.py times), sampled heads against the oracle; a second call gives the
+    50; the shape bench.py times), every head against the oracle; a second call gives the
     same O bit for bit."""
-    p, dev, out = run_decode(32, 16, 8, 8192, 256, seed=37, heads=[0, 255, 511], softcap=50.0)
+    p, dev, out = run_decode(32, 16, 8, 8192, 256, seed=37, softcap=50.0)
     out2 = mxfa.decode(p, dev["q"], dev["qs"], dev["k"], dev["ks"], dev["v"], dev["vs"])
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
@@ -249,8 +255,8 @@ def test_r2_ragged_softcap_window_e3m2():
     run_case(1, 8, 2, 256, 256, 128, causal=True, outlier_p=0.01, seed=43, p_rule=mxfa.P_R2)
 
 
-def test_r2_config3_sampled_heads():
-    run_case(2, 32, 8, 4096, 4096, 128, causal=True, outlier_p=0.01, seed=44, heads=[7, 40], check_codes=False,
+def test_r2_config3_all_heads():
+    run_case(2, 32, 8, 4096, 4096, 128, causal=True, outlier_p=0.01, seed=44, check_codes=False,
              p_rule=mxfa.P_R2)
 
 
