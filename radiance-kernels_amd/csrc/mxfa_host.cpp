@@ -159,10 +159,20 @@ hipFunction_t fn_by_name(DeviceModule* dm, const char* name) {
   return nullptr;
 }
 
+// MXFA_PREFILL_LDS_PAD=<bytes>: that much dynamic LDS added to every prefill launch, which
+// lowers how many workgroups share a CU without changing the code object (an occupancy
+// measurement; unset, the launches use their static LDS only)
+unsigned prefill_lds_pad(const char* name) {
+  if (std::strncmp(name, "mxfa_prefill3", 13) != 0) return 0;
+  const char* env = getenv("MXFA_PREFILL_LDS_PAD");
+  const long v = env ? atol(env) : 0;
+  return v > 0 && v <= 96 * 1024 ? (unsigned)v : 0;
+}
+
 mxfa_status launch(DeviceModule* dm, const char* name, dim3 grid, dim3 block, void** args, void* stream) {
   hipFunction_t f = fn_by_name(dm, name);
   if (!f) return fail(MXFA_ERR_MODULE, std::string("unknown kernel ") + name);
-  MXFA_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+  MXFA_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, prefill_lds_pad(name),
                                  reinterpret_cast<hipStream_t>(stream), args, nullptr));
   return MXFA_OK;
 }
