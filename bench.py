@@ -450,8 +450,9 @@ def profile_workload(torch, mxfa, name, args):
                         args.steps, args.warmup, preheat=False)
         print(json.dumps({"profile": name, "ms_per_call": round(ms, 4), "calls": args.steps + args.warmup}), flush=True)
         return
-    elif name == "gemm":
-        M, K, N = 8192, 4096, 6144           # bench_gemm's QKV projection, fp32 C
+    elif name in ("gemm", "gemm64"):
+        # bench_gemm's QKV projection, fp32 C; gemm64: the same weights at decode batch M = 64
+        M, K, N = (8192 if name == "gemm" else 64), 4096, 6144
         X = torch.empty((M, K), dtype=torch.float32, device=dev)
         W = torch.empty((K, N), dtype=torch.float32, device=dev)
         mxfa.fill_normal(X, 41)
@@ -485,7 +486,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="only run a 256 MiB device copy x3")
     ap.add_argument("--profile", metavar="WORKLOAD",
-                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode, decode256, gemm): W untimed + K timed calls")
+                    help="run one workload alone for rocprofv3 (c1, c2, c3, c3r2, c4, decode, decode256, gemm, gemm64): W untimed + K timed calls")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus must be 1 (the path is not sharded across GPUs here)",

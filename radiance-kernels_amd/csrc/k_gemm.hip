@@ -588,38 +588,60 @@ __device__ void gemm_skinny_impl(const GemmArgs& g) {
   uint8_t* const ssa = scales;                                     // [K / 32][M]
   uint8_t* const ssb = scales + kb * g.M;                          // [K / 32][32]: the strip's columns
 
+  // The scales go to LDS first: SA whole, then the strip's 32 bytes of each SB row (M % 16 ==
+  // 0 and N % 16 == 0 keep every dword aligned; columns >= N read 0).  Their first batch is
+  // issued before the operand ring, so that its stores wait for those loads only (vmcnt
+  // counts in order) while the ring's loads stay in flight.  Loads past the arrays get bit 31
+  // of the offset (no branch).
+  const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(g.sa, 0, (int64_t)kb * g.M);
+  const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(g.sb, 0, (int64_t)kb * g.N);
+  const int na = kb * g.M / 4, nb = kb * 8;
+  constexpr int BA = 16, BB = 8;                                   // dwords per thread per batch
+  uint32_t* const sw = reinterpret_cast<uint32_t*>(scales);
+  uint32_t va[BA], vb[BB];
+  auto load_sa = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < BA; u++) {
+      const int d = base + tid + 256 * u;
+      va[u] = __builtin_amdgcn_raw_buffer_load_b32(rsa, (uint32_t)(4 * d) | ((uint32_t)(d >= na) << 31), 0, 0);
+    }
+  };
+  auto store_sa = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < BA; u++)
+      if (base + tid + 256 * u < na) sw[base + tid + 256 * u] = va[u];
+  };
+  auto load_sb = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < BB; u++) {
+      const int e = base + tid + 256 * u, row = e >> 3, col = n0 + 4 * (e & 7);
+      const uint32_t so = (uint32_t)(row * g.N + col) | ((uint32_t)(col >= g.N || e >= nb) << 31);
+      vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rsb, so, 0, 0);
+    }
+  };
+  auto store_sb = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < BB; u++)
+      if (base + tid + 256 * u < nb) sw[na + base + tid + 256 * u] = vb[u];
+  };
+  load_sa(0);
+  load_sb(0);
+
   SkinnySlot<T> ring[R];
 #pragma unroll
   for (int j = 0; j < R; j++) {
     skinny_load<T>(ring[j], g, ra, rb, wave + 4 * j, wave + 4 * j < nsteps, n0, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
-  {
-    // the scales, in batches of 8 dwords per thread (all loads of a batch before its stores;
-    // M % 16 == 0 and N % 16 == 0 keep every dword aligned): SA whole, then the strip's 32
-    // bytes of each SB row (columns >= N read 0)
-    const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(g.sa, 0, (int64_t)kb * g.M);
-    const __amdgpu_buffer_rsrc_t rsb = buf_rsrc(g.sb, 0, (int64_t)kb * g.N);
-    const int na = kb * g.M / 4, nb = kb * 8;
-    for (int base = tid; base < na + nb; base += 256 * 8) {
-      uint32_t v[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int d = base + 256 * u;
-        if (d < na) {
-          v[u] = __builtin_amdgcn_raw_buffer_load_b32(rsa, 4 * d, 0, 0);
-        } else {
-          const int e = d - na, row = e >> 3, col = n0 + 4 * (e & 7);
-          const uint32_t so = (uint32_t)(row * g.N + col) | ((uint32_t)(col >= g.N || e >= nb) << 31);
-          v[u] = __builtin_amdgcn_raw_buffer_load_b32(rsb, so, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int d = base + 256 * u;
-        if (d < na + nb) reinterpret_cast<uint32_t*>(scales)[d] = v[u];
-      }
-    }
+  store_sa(0);
+  store_sb(0);
+  for (int base = 256 * BA; base < na; base += 256 * BA) {
+    load_sa(base);
+    store_sa(base);
+  }
+  for (int base = 256 * BB; base < nb; base += 256 * BB) {
+    load_sb(base);
+    store_sb(base);
   }
   __syncthreads();
 
