@@ -484,8 +484,11 @@ extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_dma(GemmArgs g) {
 // is its own registers and every wait is a partial vmcnt):
 //   B   k rows k0 + 32 q + lane / 2, 16-byte half lane % 2 of the strip (q = 0, 1; columns >= N
 //       read 0), written to the wave's 2 KB LDS slab [64 k][32] for the transposed reads
-//   A   row 32 i + lane % 32, bytes k0 + 16 h .. and k0 + 32 + 16 h .. (h = lane / 32): the MFMA
-//       operand as it is (rows >= M read 0)
+//   A   rows 32 i + 16 q + lane / 4, bytes k0 + 16 (lane % 4) .. (q = 0, 1; rows >= M read 0):
+//       whole 64-byte row pieces per four lanes, so that an instruction touches 16 rows instead
+//       of 32 (the vector L1 handles one cache line per access: M = 64 17.2 -> 13.4 us in a
+//       timing copy), then through the wave's LDS slab (rows 80 bytes apart) into the MFMA
+//       operand layout (row lane % 32, bytes 16 h .. and 32 + 16 h .., h = lane / 32)
 // The four partial accumulators are summed through LDS in wave order (deterministic) and C
 // is stored 32 consecutive columns per 32 lanes.
 // ---------------------------------------------------------------------------
@@ -495,6 +498,9 @@ constexpr int SKINNY_SCALE_BYTES = 96 * 1024;                   // (K / 32) (M +
 // 4 slots 11.3 / 17.0 / 25.7 us, the vmcnt limit (16 / 11 / 7) 14.1 / 18.2 / 26.4 us.
 template <int T> struct SkinnyCfg {
   static constexpr int R = T == 1 ? 8 : T == 2 ? 6 : 4;
+  static constexpr int AP = 80;                                  // A row pitch in the slab (bytes)
+  static constexpr int SLAB = 2048 + T * 32 * AP;                // per-wave slab: B [64][32], A tiles
+  static_assert(4 * SLAB >= 4 * 16 * 64 * 4, "the partials reuse the slabs");
   static_assert((R - 1) * (2 + 2 * T) <= 63, "vmcnt range");
 };
 
@@ -508,7 +514,7 @@ template <int T> struct SkinnySlot {
 template <int T>
 __device__ __forceinline__ void skinny_load(SkinnySlot<T>& sl, const GemmArgs& g, __amdgpu_buffer_rsrc_t ra,
                                             __amdgpu_buffer_rsrc_t rb, int step, bool on, int n0, int lane) {
-  const int r = lane & 31, h = lane >> 5, k0 = step * 64;
+  const int k0 = step * 64;
   const uint32_t dis = (uint32_t)!on << 31;
 #pragma unroll
   for (int q = 0; q < 2; q++) {
@@ -517,12 +523,13 @@ __device__ __forceinline__ void skinny_load(SkinnySlot<T>& sl, const GemmArgs& g
     sl.b[q] = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, 0, 0);
   }
 #pragma unroll
-  for (int i = 0; i < T; i++) {
-    const int row = 32 * i + r;
-    const uint32_t vo = (uint32_t)(row * g.K + k0 + 16 * h) | dis | ((uint32_t)(row >= g.M) << 31);
-    sl.a[i][0] = __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0);
-    sl.a[i][1] = __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 32, 0, 0);
-  }
+  for (int i = 0; i < T; i++)
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      const int row = 32 * i + 16 * q + (lane >> 2);
+      const uint32_t vo = (uint32_t)(row * g.K + k0 + 16 * (lane & 3)) | dis | ((uint32_t)(row >= g.M) << 31);
+      sl.a[i][q] = __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0);
+    }
 }
 
 template <int T>
@@ -541,10 +548,22 @@ __device__ __forceinline__ void skinny_mma(v16f (&acc)[T], const SkinnySlot<T>& 
     bo[2 * q] = t[0];
     bo[2 * q + 1] = t[1];
   }
-  const int sb = ssb[(2 * step + h) * 32 + r];
+  // A tiles [32 rows][64 bytes] at row pitch AP: the loaded row pieces, then each lane's two
+  // 16-byte operand pieces
+  constexpr int AP = SkinnyCfg<T>::AP;
+  uint8_t* const as = slab + 2048;
 #pragma unroll
   for (int i = 0; i < T; i++)
-    acc[i] = mfma_mx(cat44(sl.a[i][0], sl.a[i][1]), bo, acc[i], ssa[(2 * step + h) * M + 32 * i + r], sb);
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+      *reinterpret_cast<v4i*>(as + i * 32 * AP + (16 * q + (lane >> 2)) * AP + 16 * (lane & 3)) = sl.a[i][q];
+  const int sb = ssb[(2 * step + h) * 32 + r];
+#pragma unroll
+  for (int i = 0; i < T; i++) {
+    const uint8_t* ar = as + i * 32 * AP + r * AP + 16 * h;
+    acc[i] = mfma_mx(cat44(*reinterpret_cast<const v4i*>(ar), *reinterpret_cast<const v4i*>(ar + 32)), bo, acc[i],
+                     ssa[(2 * step + h) * M + 32 * i + r], sb);
+  }
 }
 
 template <int T, int... J>
@@ -571,9 +590,9 @@ __device__ __forceinline__ void skinny_tail(v16f (&acc)[T], SkinnySlot<T> (&ring
 template <int T>
 __device__ void gemm_skinny_impl(const GemmArgs& g) {
   constexpr int R = SkinnyCfg<T>::R;
-  __shared__ __attribute__((aligned(16))) uint8_t slabs[4 * 2048];
+  __shared__ __attribute__((aligned(16))) uint8_t slabs[4 * SkinnyCfg<T>::SLAB];
   __shared__ __attribute__((aligned(16))) uint8_t scales[SKINNY_SCALE_BYTES];
-  __shared__ __attribute__((aligned(16))) float part[4 * 16 * 64];
+  float* const part = reinterpret_cast<float*>(slabs);          // after the loop
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nstrips = (g.N + 31) / 32;
   const int nwg = (int)gridDim.x, lin = (int)blockIdx.x;
@@ -584,7 +603,7 @@ __device__ void gemm_skinny_impl(const GemmArgs& g) {
   const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, 0, (int64_t)g.M * g.K);
   const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, 0, (int64_t)g.K * g.N);
   const int nsteps = g.K / 64, kb = g.K / 32;
-  uint8_t* const slab = slabs + 2048 * wave;
+  uint8_t* const slab = slabs + SkinnyCfg<T>::SLAB * wave;
   uint8_t* const ssa = scales;                                     // [K / 32][M]
   uint8_t* const ssb = scales + kb * g.M;                          // [K / 32][32]: the strip's columns
 
@@ -654,7 +673,9 @@ __device__ void gemm_skinny_impl(const GemmArgs& g) {
   for (int round = 0; round < mine / R; round++, step0 += 4 * R)
     skinny_round<T>(acc, ring, g, ra, rb, slab, ssa, ssb, step0, nsteps, n0, lane, std::make_integer_sequence<int, R>{});
   skinny_tail<T>(acc, ring, slab, ssa, ssb, g.M, step0, mine % R, lane, std::make_integer_sequence<int, R - 1>{});
-  // the four partials of each row tile, summed in wave order
+  // the four partials of each row tile, summed in wave order (in the slabs: every wave is past
+  // its last operand reads first)
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < T; i++) {
 #pragma unroll
