@@ -96,6 +96,10 @@ def test_decode_validation_and_plan():
     assert mxfa.decode_plan(mxfa.make_params(1, 8, 1, 1, 64 * 40, 64, causal=True, q_pos0=2559))[0] == 40
     assert mxfa.decode_plan(mxfa.make_params(8, 32, 8, 1, 4096, 128, causal=True, q_pos0=4095))[0] == 32
     assert mxfa.decode_plan(mxfa.make_params(96, 32, 8, 1, 4096, 128, causal=True, q_pos0=4095))[0] == 4
+    # D = 256 (one workgroup per CU): about 1,024 partial waves, half the D <= 128 target
+    assert mxfa.decode_plan(mxfa.make_params(32, 16, 8, 1, 8192, 256, causal=True, q_pos0=8191))[0] == 4
+    assert mxfa.decode_plan(mxfa.make_params(32, 16, 8, 1, 8192, 128, causal=True, q_pos0=8191))[0] == 8
+    assert mxfa.decode_plan(mxfa.make_params(2, 16, 8, 1, 8192, 256, causal=True, q_pos0=8191))[0] == 64
     p2 = mxfa.make_params(1, 1, 1, 2, 64, 64)
     sl_ = ctypes.c_int32(0)
     ws_ = ctypes.c_size_t(0)
