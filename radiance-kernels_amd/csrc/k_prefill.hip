@@ -15,56 +15,55 @@
 //   DMA K_bf16(j+1), V(j+1) into the other stage -> scores of j (bf16 MFMA) -> mask ->
 //   softmax + P requant -> O rescale -> PV (scaled MXFP8 MFMA) -> wait, barrier.
 // ---------------------------------------------------------------------------
-// Workspace pre-pass: each thread converts PRE_G chunks of 16 codes (one 32-block half) of
-// one (batch, KV head) -- blockIdx.y -- the workgroup's 256 * PRE_G consecutive chunks of
-// that head, all loads issued before the stores (PRE_G = 8: 8.7 vs 10.2 us on the S = 4096
-// GQA prefill, one workgroup per CU; 2 and 4 were slower).  D / 16 chunks per row (4, 8 or
-// 16) divides 256, so a thread's chunks share one column and step 256 / (D / 16) rows.
+// Workspace pre-pass: each thread converts PRE_G pieces of 8 codes (a quarter 32-block) of
+// one (batch, KV head) -- blockIdx.y -- the workgroup's 256 * PRE_G consecutive pieces of
+// that head, all loads issued before the stores.  A piece widens to 16 bytes of bf16, so each
+// store instruction writes 1 KB of whole lines (16-byte pieces, each widened into two 16-byte
+// stores 32 bytes apart, wrote every line half per instruction: 8.2 vs 7.9 us on the S = 4096
+// GQA prefill).  D / 8 pieces per row (8, 16
+// or 32) divides 256, so a thread's pieces share one column and step 256 / (D / 8) rows.
 // Row t of head h in the copies is row h * Skc + t of the cache-strided input: the bf16 value
 // of K (kbf) and, when vws is set, the E4M3 code of E3M2 V (e3m2x4_to_e4m3x4: the same
 // value) -- one launch for both.
-constexpr int PRE_G = 8;
+constexpr int PRE_G = 16;
+
 extern "C" __global__ void __launch_bounds__(256) mxfa_k_to_bf16(const uint8_t* __restrict__ k,
                                                                   const uint8_t* __restrict__ ks,
                                                                   const uint8_t* __restrict__ v, int D, int Sk,
                                                                   int Skc, uint8_t* __restrict__ kbf,
                                                                   uint8_t* __restrict__ vws) {
-  const int lcpr = D == 256 ? 4 : D == 128 ? 3 : 2;
-  const int c0 = blockIdx.x * blockDim.x * PRE_G + threadIdx.x;   // chunk within the head
-  const int col = c0 & ((1 << lcpr) - 1);
-  const int rstep = (int)blockDim.x >> lcpr;
-  const int t0 = c0 >> lcpr;
+  const int lppr = D == 256 ? 5 : D == 128 ? 4 : 3;               // log2 of pieces per row
+  const int c0 = blockIdx.x * blockDim.x * PRE_G + threadIdx.x;   // piece within the head
+  const int col = c0 & ((1 << lppr) - 1);
+  const int rstep = (int)blockDim.x >> lppr;
+  const int t0 = c0 >> lppr;
   const int64_t hq = blockIdx.y;
-  int64_t so[PRE_G], doff[PRE_G];   // source and copy byte offsets of chunk g (past the end: row 0)
-  v4i x[PRE_G];
+  int64_t so[PRE_G], doff[PRE_G];   // source and copy byte offsets of piece g (past the end: row 0)
+  v2i x[PRE_G];
   float sc[PRE_G];
 #pragma unroll
   for (int g = 0; g < PRE_G; g++) {
     const int t = t0 + g * rstep;
     const int64_t src = t < Sk ? hq * Skc + t : 0;
-    so[g] = src * D + col * 16;
-    doff[g] = (hq * Sk + t) * D + col * 16;
-    x[g] = *reinterpret_cast<const v4i*>(k + so[g]);
-    sc[g] = e8m0_as_float(ks[src * (D / 32) + col / 2]);
+    so[g] = src * D + col * 8;
+    doff[g] = (hq * Sk + t) * D + col * 8;
+    x[g] = *reinterpret_cast<const v2i*>(k + so[g]);
+    sc[g] = e8m0_as_float(ks[src * (D / 32) + col / 4]);
   }
 #pragma unroll
-  for (int g = 0; g < PRE_G; g++) {
-    if (t0 + g * rstep < Sk) {
-      v4i* o = reinterpret_cast<v4i*>(kbf + doff[g] * 2);
-      o[0] = fp8x8_to_bf16x8((uint32_t)x[g][0], (uint32_t)x[g][1], sc[g]);
-      o[1] = fp8x8_to_bf16x8((uint32_t)x[g][2], (uint32_t)x[g][3], sc[g]);
-    }
-  }
+  for (int g = 0; g < PRE_G; g++)
+    if (t0 + g * rstep < Sk)
+      *reinterpret_cast<v4i*>(kbf + doff[g] * 2) = fp8x8_to_bf16x8((uint32_t)x[g][0], (uint32_t)x[g][1], sc[g]);
   if (vws) {
 #pragma unroll
-    for (int g = 0; g < PRE_G; g++) x[g] = *reinterpret_cast<const v4i*>(v + so[g]);
+    for (int g = 0; g < PRE_G; g++) x[g] = *reinterpret_cast<const v2i*>(v + so[g]);
 #pragma unroll
     for (int g = 0; g < PRE_G; g++) {
       if (t0 + g * rstep < Sk) {
-        v4i z;
-#pragma unroll
-        for (int w = 0; w < 4; w++) z[w] = (int)e3m2x4_to_e4m3x4((uint32_t)x[g][w]);
-        *reinterpret_cast<v4i*>(vws + doff[g]) = z;
+        v2i z;
+        z[0] = (int)e3m2x4_to_e4m3x4((uint32_t)x[g][0]);
+        z[1] = (int)e3m2x4_to_e4m3x4((uint32_t)x[g][1]);
+        *reinterpret_cast<v2i*>(vws + doff[g]) = z;
       }
     }
   }

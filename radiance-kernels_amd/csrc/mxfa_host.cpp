@@ -607,12 +607,12 @@ mxfa_status prefill_ws_impl(const mxfa_attn_params* p, const uint8_t* q, const u
   uint8_t* vws = p->v_fmt == MXFA_FMT_E3M2 ? kbf + prefill3_kbf_bytes(p) : nullptr;
   a.kbf = kbf;
   a.vws = vws;
-  // bf16 K (and E4M3 V) in one launch: 8 chunks of 16 codes per thread, one (batch, KV head)
+  // bf16 K (and E4M3 V) in one launch: 16 pieces of 8 codes per thread, one (batch, KV head)
   // per grid row
   int D = p->head_dim, Sk = p->seq_k, Skc = a.Skc;
-  const int64_t chunks = (int64_t)Sk * (D / 16);   // per (batch, KV head)
-  if (chunks > INT32_MAX - 256 * 8) return fail(MXFA_ERR_UNSUPPORTED, "seq_k * head_dim / 16 exceeds the workspace pre-pass's range");
-  const dim3 cgrid((unsigned)((chunks + 256 * 8 - 1) / (256 * 8)), (unsigned)(p->batch * p->num_kv_heads));
+  const int64_t pieces = (int64_t)Sk * (D / 8);    // per (batch, KV head)
+  if (pieces > INT32_MAX - 256 * 16) return fail(MXFA_ERR_UNSUPPORTED, "seq_k * head_dim / 8 exceeds the workspace pre-pass's range");
+  const dim3 cgrid((unsigned)((pieces + 256 * 16 - 1) / (256 * 16)), (unsigned)(p->batch * p->num_kv_heads));
   void* cargs[] = {(void*)&k, (void*)&k_sc, (void*)&v, &D, &Sk, &Skc, &kbf, &vws};
   if (mxfa_status st = launch(dm, "mxfa_k_to_bf16", cgrid, dim3(256), cargs, stream)) return st;
   void* args[] = {&a};
