@@ -312,47 +312,80 @@ template <int NW>
 __device__ __forceinline__ int gemm_dma_swa(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int gemm_dma_swb(int krow) { return 2 * (krow & 7); }
 
+// The MFMA operands of one step, read from LDS one MFMA pair ahead of their use: the B
+// operand of a 64-k half (TJ column tiles, eight k rows per ds_read_b64_tr_b8) and the A
+// operand of one 32-row tile, each with its E8M0 scales.
+template <int NW> struct GemmOpB {
+  v8i b[GemmCfg<NW>::TJ];
+  int s[GemmCfg<NW>::TJ];
+};
+struct GemmOpA {
+  v8i a;
+  int s;
+};
+
 template <int NW>
-__device__ __forceinline__ void gemm_mma_dma(v16f (&acc)[4][GemmCfg<NW>::TJ], const uint8_t* sA, const uint8_t* sB,
-                                             const uint8_t* sS, int wr, int wc, int lane) {
+__device__ __forceinline__ void gemm_read_b(GemmOpB<NW>& o, const uint8_t* sB, const uint8_t* sS, int kh, int wc,
+                                            int lane) {
   using namespace gemm;
   constexpr int TJ = GemmCfg<NW>::TJ;
   const int r = lane & 31, h = lane >> 5, l16 = lane & 15, g16 = lane >> 4;
-  bool first = NW == 8;
+#pragma unroll
+  for (int j = 0; j < TJ; j++) {
+    const int ncol = 32 * TJ * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int krow = 64 * kh + 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
+      const int addr = krow * TN + ((((ncol >> 4) ^ gemm_dma_swb(krow))) << 4) + (ncol & 15);
+      v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB + addr));
+      o.b[j][2 * q] = t[0];
+      o.b[j][2 * q + 1] = t[1];
+    }
+    o.s[j] = sS[KB * TM + (2 * kh + h) * TN + 32 * TJ * wc + 32 * j + r];
+  }
+}
+
+template <int NW>
+__device__ __forceinline__ void gemm_read_a(GemmOpA& o, const uint8_t* sA, const uint8_t* sS, int kh, int i, int wr,
+                                            int lane) {
+  using namespace gemm;
+  const int r = lane & 31, h = lane >> 5;
+  const int row = 128 * wr + 32 * i + r;
+  const int sw = gemm_dma_swa<NW>(row);
+  const v4i lo = *reinterpret_cast<const v4i*>(sA + row * TK + (((4 * kh + h) ^ sw) << 4));
+  const v4i hi = *reinterpret_cast<const v4i*>(sA + row * TK + (((4 * kh + 2 + h) ^ sw) << 4));
+  o.a = cat44(lo, hi);
+  o.s = sS[(2 * kh + h) * TM + row];
+}
+
+// One step's MFMAs on the stage (sA, sB, sS).  On entry a holds the A operand of (k half 0,
+// tile 0) and b0 the B operand of k half 0; the B operand of half 1 is read first, and each A
+// operand is read while the MFMA pair before it is issued, so that a wave's MFMA chain waits
+// on LDS only at the start of the tile (the other wave of the SIMD covers that).
+template <int NW>
+__device__ __forceinline__ void gemm_mma_dma(v16f (&acc)[4][GemmCfg<NW>::TJ], GemmOpA& a, const GemmOpB<NW>& b0,
+                                             const uint8_t* sA, const uint8_t* sB, const uint8_t* sS, int wr, int wc,
+                                             int lane) {
+  using namespace gemm;
+  constexpr int TJ = GemmCfg<NW>::TJ;
+  GemmOpB<NW> b1;
+  gemm_read_b<NW>(b1, sB, sS, 1, wc, lane);
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int kh = 0; kh < TK / 64; kh++) {
-    v8i bo[TJ];
-    int bsc[TJ];
-#pragma unroll
-    for (int j = 0; j < TJ; j++) {
-      const int ncol = 32 * TJ * wc + 32 * j + 16 * (g16 & 1) + 8 * (l16 & 1);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int krow = 64 * kh + 32 * (q >> 1) + 16 * h + 8 * (q & 1) + (l16 >> 1);
-        const int addr = krow * TN + ((((ncol >> 4) ^ gemm_dma_swb(krow))) << 4) + (ncol & 15);
-        v2i t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(sB + addr));
-        bo[j][2 * q] = t[0];
-        bo[j][2 * q + 1] = t[1];
-      }
-      bsc[j] = sS[KB * TM + (2 * kh + h) * TN + 32 * TJ * wc + 32 * j + r];
-    }
+    const GemmOpB<NW>& b = kh ? b1 : b0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int row = 128 * wr + 32 * i + r;
-      const int sw = gemm_dma_swa<NW>(row);
-      const v4i lo = *reinterpret_cast<const v4i*>(sA + row * TK + (((4 * kh + h) ^ sw) << 4));
-      const v4i hi = *reinterpret_cast<const v4i*>(sA + row * TK + (((4 * kh + 2 + h) ^ sw) << 4));
-      const v8i ao = cat44(lo, hi);
-      const int asc = sS[(2 * kh + h) * TM + row];
-      if (first) {
-        __builtin_amdgcn_s_setprio(1);
-        first = false;
-      }
+      GemmOpA an;
+      if (i < 3) gemm_read_a<NW>(an, sA, sS, kh, i + 1, wr, lane);
+      else if (kh == 0) gemm_read_a<NW>(an, sA, sS, 1, 0, wr, lane);
+      __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the MFMAs (own registers)
 #pragma unroll
-      for (int j = 0; j < TJ; j++) acc[i][j] = mfma_mx(ao, bo[j], acc[i][j], asc, bsc[j]);
+      for (int j = 0; j < TJ; j++) acc[i][j] = mfma_mx(a.a, b.b[j], acc[i][j], a.s, b.s[j]);
+      if (i < 3 || kh == 0) a = an;
     }
   }
-  if (NW == 8) __builtin_amdgcn_s_setprio(0);
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // The DMA of one step into a stage: wave w issues A and B instructions w * IPW .. + IPW - 1
@@ -435,14 +468,24 @@ __device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
   gemm_dma<NW>(g, ra, rb, rs, dl, sA0, sB0, sS0, wave, 0);
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
   __syncthreads();
+  GemmOpA a;
+  GemmOpB<NW> b0;
+  gemm_read_b<NW>(b0, sB0, sS0, 0, wc, lane);
+  gemm_read_a<NW>(a, sA0, sS0, 0, 0, wr, lane);
   auto step = [&](auto stc, int kt) {
     constexpr int ST = decltype(stc)::value;
     // the next step's tiles into the other stage (the last step reloads itself: in bounds,
     // never multiplied)
     gemm_dma<NW>(g, ra, rb, rs, dl, ST ? sA0 : sA1, ST ? sB0 : sB1, ST ? sS0 : sS1, wave, min(kt + 1, nk - 1) * TK);
-    gemm_mma_dma<NW>(acc, ST ? sA1 : sA0, ST ? sB1 : sB0, ST ? sS1 : sS0, wr, wc, lane);
-    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0000 | 0);   // vmcnt(0) lgkmcnt(0)
+    gemm_mma_dma<NW>(acc, a, b0, ST ? sA1 : sA0, ST ? sB1 : sB0, ST ? sS1 : sS0, wr, wc, lane);
+    // the stage just multiplied is free and the next one has landed once every wave is here;
+    // the next step's first operands are read while this step's last MFMAs run (no DMA is in
+    // flight across the loop's back edge, so the compiler's per-buffer DMA tracking holds)
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 0);   // vmcnt(0)
     __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");                 // no LDS read moves above the barrier
+    gemm_read_b<NW>(b0, ST ? sB0 : sB1, ST ? sS0 : sS1, 0, wc, lane);
+    gemm_read_a<NW>(a, ST ? sA0 : sA1, ST ? sS0 : sS1, 0, 0, wr, lane);
   };
   for (int kt = 0; kt < nk; kt += 2) {
     step(std::integral_constant<int, 0>{}, kt);
