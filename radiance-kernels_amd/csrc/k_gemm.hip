@@ -362,10 +362,10 @@ __device__ __forceinline__ void gemm_read_a(GemmOpA& o, const uint8_t* sA, const
 // tile 0) and b0 the B operand of k half 0; the B operand of half 1 is read first, and each A
 // operand is read while the MFMA pair before it is issued, so that a wave's MFMA chain waits
 // on LDS only at the start of the tile (the other wave of the SIMD covers that).
-template <int NW>
+template <int NW, typename Dma>
 __device__ __forceinline__ void gemm_mma_dma(v16f (&acc)[4][GemmCfg<NW>::TJ], GemmOpA& a, const GemmOpB<NW>& b0,
                                              const uint8_t* sA, const uint8_t* sB, const uint8_t* sS, int wr, int wc,
-                                             int lane) {
+                                             int lane, const Dma& dma) {
   using namespace gemm;
   constexpr int TJ = GemmCfg<NW>::TJ;
   GemmOpB<NW> b1;
@@ -382,6 +382,10 @@ __device__ __forceinline__ void gemm_mma_dma(v16f (&acc)[4][GemmCfg<NW>::TJ], Ge
       __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the MFMAs (own registers)
 #pragma unroll
       for (int j = 0; j < TJ; j++) acc[i][j] = mfma_mx(a.a, b.b[j], acc[i][j], a.s, b.s[j]);
+      if (kh == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        dma(i);   // the next step's DMA, a quarter behind each MFMA group of the first k half
+      }
       if (i < 3 || kh == 0) a = an;
     }
   }
@@ -389,28 +393,36 @@ __device__ __forceinline__ void gemm_mma_dma(v16f (&acc)[4][GemmCfg<NW>::TJ], Ge
 }
 
 // The DMA of one step into a stage: wave w issues A and B instructions w * IPW .. + IPW - 1
-// (IPW = 32 / NW; instruction i covers A rows 8i .. 8i + 7 and B k rows 4i .. 4i + 3) and one
-// scale row: SA row kb = w % KB (waves < NW / 2) or SB row (the others); with NW = 8 that is
-// every scale row once.
+// (IPW = 32 / NW; instruction i covers A rows 8i .. 8i + 7 and B k rows 4i .. 4i + 3) and SR =
+// 2 KB / NW scale rows: SA rows (waves < NW / 2) or SB rows (the others), kb = (w SR + u) % KB,
+// so that every scale row is loaded once.
 struct GemmDmaLane {
   uint32_t a[2], b[2], s;   // vector offsets (A and B by instruction parity: the swizzle alternates)
 };
 
-template <int NW>
+// Part `part` of NP issues the wave's A and B instructions q = part IPW / NP .. and, in part 0,
+// its scale rows.
+template <int NW, int NP = 1>
 __device__ __forceinline__ void gemm_dma(const GemmArgs& g, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                          __amdgpu_buffer_rsrc_t rs, const GemmDmaLane& dl, uint8_t* sA, uint8_t* sB,
-                                         uint8_t* sS, int wave, int k0) {
+                                         uint8_t* sS, int wave, int k0, int part = 0) {
   using namespace gemm;
   constexpr int IPW = 32 / NW;
+  static_assert(IPW % NP == 0, "DMA parts");
 #pragma unroll
-  for (int q = 0; q < IPW; q++) {
+  for (int q = part * (IPW / NP); q < (part + 1) * (IPW / NP); q++) {
     const int i = wave * IPW + q;
     dma_lds<16>(ra, sA + i * 1024, dl.a[i & 1], 8 * i * g.K + k0);
     dma_lds<16>(rb, sB + i * 1024, dl.b[i & 1], (k0 + 4 * i) * g.N);
   }
+  constexpr int SR = 2 * KB / NW;
   const bool is_a = wave < NW / 2;
-  const int kb = wave % KB;
-  dma_lds<4>(rs, sS + (is_a ? kb * TM : KB * TM + kb * TN), dl.s, (k0 / 32 + kb) * (is_a ? g.M : g.N));
+  if (part != 0) return;
+#pragma unroll
+  for (int u = 0; u < SR; u++) {
+    const int kb = (wave * SR + u) % KB;
+    dma_lds<4>(rs, sS + (is_a ? kb * TM : KB * TM + kb * TN), dl.s, (k0 / 32 + kb) * (is_a ? g.M : g.N));
+  }
 }
 
 template <int NW>
@@ -418,7 +430,7 @@ __device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
   using namespace gemm;
   using C = GemmCfg<NW>;
   constexpr int TJ = C::TJ;
-  static_assert(NW == 8, "DMA staging: eight waves (one scale row each)");
+  static_assert(NW == 4 || NW == 8, "DMA staging: four or eight waves");
   __shared__ __attribute__((aligned(16))) uint8_t sA0[TM * TK];
   __shared__ __attribute__((aligned(16))) uint8_t sA1[TM * TK];
   __shared__ __attribute__((aligned(16))) uint8_t sB0[TK * TN];
@@ -476,8 +488,11 @@ __device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
     constexpr int ST = decltype(stc)::value;
     // the next step's tiles into the other stage (the last step reloads itself: in bounds,
     // never multiplied)
-    gemm_dma<NW>(g, ra, rb, rs, dl, ST ? sA0 : sA1, ST ? sB0 : sB1, ST ? sS0 : sS1, wave, min(kt + 1, nk - 1) * TK);
-    gemm_mma_dma<NW>(acc, a, b0, ST ? sA1 : sA0, ST ? sB1 : sB0, ST ? sS1 : sS0, wr, wc, lane);
+    const int kn = min(kt + 1, nk - 1) * TK;
+    auto dma = [&](int part) {
+      gemm_dma<NW, 4>(g, ra, rb, rs, dl, ST ? sA0 : sA1, ST ? sB0 : sB1, ST ? sS0 : sS1, wave, kn, part);
+    };
+    gemm_mma_dma<NW>(acc, a, b0, ST ? sA1 : sA0, ST ? sB1 : sB0, ST ? sS1 : sS0, wr, wc, lane, dma);
     // the stage just multiplied is free and the next one has landed once every wave is here;
     // the next step's first operands are read while this step's last MFMAs run (no DMA is in
     // flight across the loop's back edge, so the compiler's per-buffer DMA tracking holds)
@@ -514,7 +529,12 @@ __device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
   }
 }
 
-extern "C" __global__ void __launch_bounds__(512, 1) mxfa_gemm_dma(GemmArgs g) { gemm_dma_impl<8>(g); }
+#ifndef MXFA_GEMM_DMA_WAVES
+#define MXFA_GEMM_DMA_WAVES 8
+#endif
+extern "C" __global__ void __launch_bounds__(64 * MXFA_GEMM_DMA_WAVES, 1) mxfa_gemm_dma(GemmArgs g) {
+  gemm_dma_impl<MXFA_GEMM_DMA_WAVES>(g);
+}
 
 // ---------------------------------------------------------------------------
 // Skinny MX GEMM (M <= 32 T rows, E4M3 x E4M3): the batched-decode projection, where the big
