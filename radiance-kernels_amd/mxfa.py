@@ -159,6 +159,12 @@ def _ptr(t):
 def _stream(stream):
     if stream is None:
         import torch
+        # the raw handle of torch's current stream on the current device, read without building
+        # a Stream object (a few microseconds per call, which short kernels such as the
+        # decode-batch GEMM would otherwise wait on)
+        raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+        if raw is not None:
+            return ctypes.c_void_p(raw(torch._C._cuda_getDevice()))
         return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     return ctypes.c_void_p(stream if isinstance(stream, int) else stream.cuda_stream)
 
