@@ -1,5 +1,7 @@
 """GPU parity of the MX quantizers and of the attention kernels' softmax-requant step:
 bit-exact against the oracle (rule R1 of lib/golden, pinned in test_oracle_rules)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -276,6 +278,17 @@ def test_fill_normal_statistics():
     z = torch.empty(1 << 10, dtype=torch.float32, device=DEV)
     mxfa.fill_normal(z, 7)
     np.testing.assert_array_equal(np_(z), a[:1 << 10].astype(np.float32))   # counter-based: prefix-stable
+
+
+def test_quantize_rows_r4_reference_fixture():
+    """Rule R4 on the GPU against the fixture written from the reference's own golden.py
+    bit primitives (tests/golden/make_r4_golden.py): tiny-amax blocks where the reference's
+    2^-e multiplier word wraps, the normal range and amax around 448 * 2^k."""
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "r4_blocks.npz"))
+    x = np.ascontiguousarray(z["x"].reshape(-1, 64))
+    codes, scales = mxfa.quantize_rows_r4(torch.from_numpy(x).to(DEV))
+    np.testing.assert_array_equal(np_(scales).reshape(-1), z["scales"])
+    np.testing.assert_array_equal(np_(codes).reshape(-1, 32), z["codes"])
 
 
 def test_quantize_rows_r4_bit_exact():

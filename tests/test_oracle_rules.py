@@ -4,7 +4,8 @@ Pins, in order of strength:
   * committed fixtures written from the reference's own lib/golden code
     (tests/golden/make_golden.py): decode tables, the E3M2 encoder over all
     65536 bf16 patterns, the E4M3 encoder on edge cases, and the mx_golden
-    CLI's block-32 requant post-pass (codes + E8M0 scales);
+    CLI's block-32 requant post-pass (codes + E8M0 scales), and rule R4 from the
+    reference's golden.py bit primitives (tests/golden/make_r4_golden.py);
   * the reference's compiled code itself (oracle/_ref) where it was built;
   * closed forms: the OCP E4M3/E3M2 grids, libm's floorf(log2f(x)) over every
     positive float, and scale-range invariants.
@@ -232,6 +233,20 @@ def test_r4_scale_is_ceil_log2_amax_over_448():
         assert s == min(max(e + 127, 0), 254), (a, s, e)
     _, sc0 = O.r4_quantize_rows(np.zeros((1, 32), np.float32))
     assert sc0[0, 0] == 0
+
+
+def test_r4_matches_reference_golden_fixture():
+    """R4 against the reference's own bit primitives (lib/golden/golden.py block_exp,
+    pow2_neg_e, fp8_code_rshift, composed per block as kernels/simt_quant/gen_quant.py:54-70;
+    tests/golden/make_r4_golden.py): blocks whose amax is an fp32 subnormal or a normal below
+    2^-120 (where the reference's (127 - e) << 23 multiplier word wraps), the normal range
+    and amax at / around 448 * 2^k -- codes and scales bit for bit."""
+    z = np.load(os.path.join(GOLD, "r4_blocks.npz"))
+    codes, scales = O.r4_quantize_rows(z["x"])
+    np.testing.assert_array_equal(scales.reshape(-1), z["scales"])
+    np.testing.assert_array_equal(codes, z["codes"])
+    # the fixture reaches the wrapped multiplier: scale code 0 with nonzero inputs
+    assert np.any((z["scales"] == 0) & np.any(z["x"] != 0, axis=1))
 
 
 # ---- rule R2: the reference device kernels' truncating P requant
