@@ -179,6 +179,14 @@ mxfa_status launch(DeviceModule* dm, const char* name, dim3 grid, dim3 block, vo
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A launch's x extent in work-items (grid.x * block.x) is a 32-bit count in the dispatch
+// packet: a call that would need more is refused before any device work.
+mxfa_status check_grid(int64_t blocks, int threads) {
+  if (blocks * threads > (int64_t)UINT32_MAX)
+    return fail(MXFA_ERR_UNSUPPORTED, "the call needs more than 2^32 work-items in one launch: split it");
+  return MXFA_OK;
+}
+
 mxfa_status check_params(const mxfa_attn_params* p, bool decode) {
   if (!p) return fail(MXFA_ERR_INVALID_ARG, "params is NULL");
   if (p->batch < 1 || p->num_q_heads < 1 || p->num_kv_heads < 1 || p->seq_q < 1 || p->seq_k < 1)
@@ -319,10 +327,11 @@ mxfa_status mxfa_quantize_rows(const float* x, int64_t rows, int32_t cols, mxfa_
   if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
     return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte and codes 4-byte aligned");
-  DeviceModule* dm;
-  if (mxfa_status st = module_for_current(&dm)) return st;
   int64_t nblocks = rows * (int64_t)cols / 32;
   int64_t threads = nblocks * 8;
+  if (mxfa_status st = check_grid((threads + 255) / 256, 256)) return st;
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
   dim3 grid((unsigned)((threads + 255) / 256));
   void* args[] = {(void*)&x, &nblocks, &codes, &scales};
   return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_rows_e4m3" : "mxfa_quant_rows_e3m2", grid, dim3(256), args, stream);
@@ -335,9 +344,10 @@ mxfa_status mxfa_quantize_rows_r4(const float* x, int64_t rows, int32_t cols, ui
   if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
     return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte and codes 4-byte aligned");
+  int64_t nblocks = rows * (int64_t)cols / 32;
+  if (mxfa_status st = check_grid((nblocks * 8 + 255) / 256, 256)) return st;
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
-  int64_t nblocks = rows * (int64_t)cols / 32;
   void* args[] = {(void*)&x, &nblocks, &codes, &scales};
   return launch(dm, "mxfa_quant_rows_r4", dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), args, stream);
 }
@@ -351,11 +361,11 @@ mxfa_status mxfa_quantize_cols(const float* x, int64_t mats, int32_t rows, int32
   if (!x || !codes || !scales) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u) || (reinterpret_cast<uintptr_t>(scales) & 3u))
     return fail(MXFA_ERR_INVALID_ARG, "x must be 16-byte, codes and scales 4-byte aligned");
-  DeviceModule* dm;
-  if (mxfa_status st = module_for_current(&dm)) return st;
   // one wave per (matrix, 32-row block, 128 columns), four waves per workgroup
   const int64_t units = mats * (rows / 32) * ((cols + 127) / 128);
-  if ((units + 3) / 4 > INT32_MAX) return fail(MXFA_ERR_UNSUPPORTED, "mxfa_quantize_cols: too many 32 x 128 blocks");
+  if (mxfa_status st = check_grid((units + 3) / 4, 256)) return st;
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
   dim3 grid((unsigned)((units + 3) / 4));
   void* args[] = {(void*)&x, &mats, &rows, &cols, &codes, &scales};
   return launch(dm, fmt == MXFA_FMT_E4M3 ? "mxfa_quant_cols_e4m3" : fmt == MXFA_FMT_E3M2 ? "mxfa_quant_cols_e3m2"
@@ -380,19 +390,21 @@ mxfa_status mxfa_kv_append(const mxfa_kv_params* p, const float* k_new, const fl
     if (!q) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
   for (const void* q : ptrs)
     if (!aligned16(q)) return fail(MXFA_ERR_INVALID_ARG, "buffers must be 16-byte aligned");
-  DeviceModule* dm;
-  if (mxfa_status st = module_for_current(&dm)) return st;
   const int64_t bk = (int64_t)p->batch * p->num_kv_heads;
   int D = p->head_dim, L = p->max_len, n = n_new, pos = pos0;
   // one launch: K (8 lanes per 32-block) then V (one wave per 32 columns of a touched
   // 32-token block)
   int64_t kblocks = bk * n * (D / 32);
-  int kgroups = (int)((kblocks * 8 + 255) / 256);
+  const int64_t kgroups64 = (kblocks * 8 + 255) / 256;
   const int end = pos0 + n_new;
   int ntouch = (end - 1) / 32 - pos0 / 32 + 1;
   int64_t vunits = bk * ntouch * (D / 32);
   const int64_t vgroups = (vunits + 3) / 4;
-  if (kgroups + vgroups > 0x7fffffffLL) return fail(MXFA_ERR_UNSUPPORTED, "append too large for one launch");
+  if (mxfa_status st = check_grid(kgroups64 + vgroups, 256)) return st;
+  int kgroups = (int)kgroups64;
+  if (mxfa_status st = check_grid((bk * 32 * (D / 4) + 255) / 256, 256)) return st;   // the tail update
+  DeviceModule* dm;
+  if (mxfa_status st = module_for_current(&dm)) return st;
   void* args[] = {(void*)&k_new, (void*)&v_new, &v_tail, &kblocks, &kgroups, &vunits, &ntouch,
                   &n, &L, &D, &pos, &k_cache, &k_sc, &v_cache, &v_sc};
   if (mxfa_status st = launch(dm, p->v_fmt == MXFA_FMT_E4M3   ? "mxfa_kv_append_e4m3"
@@ -417,6 +429,7 @@ mxfa_status mxfa_softmax_requant(const float* s, const float* row_max, float c, 
   if (!s || !row_max || !p || !codes || !scales || !row_sum) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
   if (!aligned16(s) || (reinterpret_cast<uintptr_t>(codes) & 3u))
     return fail(MXFA_ERR_INVALID_ARG, "s must be 16-byte and codes 4-byte aligned");
+  if (mxfa_status st = check_grid((rows + 255) / 256, 256)) return st;
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
   dim3 grid((unsigned)((rows + 255) / 256));
@@ -483,6 +496,7 @@ mxfa_status mxfa_fill_normal(float* x, int64_t n, uint64_t seed, float outlier_p
   if (n < 0) return fail(MXFA_ERR_INVALID_ARG, "n must be >= 0");
   if (n == 0) return MXFA_OK;
   if (!x) return fail(MXFA_ERR_INVALID_ARG, "NULL pointer");
+  if (mxfa_status st = check_grid((n + 255) / 256, 256)) return st;
   DeviceModule* dm;
   if (mxfa_status st = module_for_current(&dm)) return st;
   dim3 grid((unsigned)((n + 255) / 256));

@@ -118,6 +118,22 @@ def test_quantize_argument_validation():
     assert L.mxfa_softmax_requant(None, None, 1.0, 0, 32, 1, None, None, None, None, None) == 0
 
 
+def test_launches_past_2_pow_32_work_items_rejected_without_device():
+    """A launch's x extent in work-items is a 32-bit count: calls that would need more are
+    MXFA_ERR_UNSUPPORTED before any device work (the pointers are never touched)."""
+    L = mxfa.lib()
+    fake = ctypes.c_void_p(1 << 20)                       # aligned, never dereferenced
+    big = 1 << 31
+    assert L.mxfa_quantize_rows(fake, big, 32, 0, fake, fake, None) == 2
+    assert b"2^32 work-items" in L.mxfa_last_error()
+    assert L.mxfa_quantize_rows_r4(fake, big, 32, fake, fake, None) == 2
+    assert L.mxfa_quantize_cols(fake, big, 32 * 1024, 128, 0, fake, fake, None) == 2
+    assert L.mxfa_softmax_requant(fake, fake, 1.0, 1 << 33, 32, 0, fake, fake, fake, fake, None) == 2
+    assert L.mxfa_fill_normal(fake, 1 << 33, 1, 0.0, 20.0, None) == 2
+    kv = mxfa.KvParams(1 << 20, 64, 256, 1 << 20, mxfa.FMT_E4M3)
+    assert L.mxfa_kv_append(ctypes.byref(kv), fake, fake, 0, 1 << 16, fake, fake, fake, fake, fake, None) == 2
+
+
 def test_kv_append_argument_validation():
     L = mxfa.lib()
     P = mxfa.KvParams
