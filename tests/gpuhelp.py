@@ -106,13 +106,21 @@ def explain_max_abs(p, dev, host, got, want, max_rows=8, rel_tie=2e-5):
     vt = _decode_table(vfmt)
     vh = host["v"] if p.v_fmt != mxfa.FMT_E3M2_BLK else mxfa.e3m2_from_blk(host["v"])
     ops = [dev[n] for n in ("q", "qs", "k", "ks", "v", "vs")]
-    op = oracle_params(p)
+    tp = p
+    if p.v_fmt == mxfa.FMT_E3M2_BLK:
+        # the stage trace and the oracle read E3M2 V one code per byte: the same codes, and P
+        # (what is traced) does not depend on V
+        import torch
+        tp = type(p).from_buffer_copy(p)
+        tp.v_fmt = mxfa.FMT_E3M2
+        ops[4] = torch.from_numpy(np.ascontiguousarray(vh)).to(dev["v"].device)
+    op = oracle_params(tp)
     bn = mxfa.DEFAULT_BLOCK_N
     group = p.num_q_heads // p.num_kv_heads
     for b, h, q in rows:
         bh = b * p.num_q_heads + h
-        tr = mxfa.prefill_trace(p, *ops, bh, q // 32)
-        ow = O.attention_trace(op, host["q"], host["qs"], host["k"], host["ks"], host["v"], host["vs"], bn, bh, q)
+        tr = mxfa.prefill_trace(tp, *ops, bh, q // 32)
+        ow = O.attention_trace(op, host["q"], host["qs"], host["k"], host["ks"], vh, host["vs"], bn, bh, q)
         r = q % 32
         vis = ~np.isneginf(ow["S"])
         nblk_sc = (np.nonzero(vis)[0].max() // 32) + 1

@@ -3,7 +3,8 @@ points accept: batch, query/KV heads (GQA groups 1-8), ragged query lengths, key
 (multiples of 32) with and without a larger kv_stride, query position offsets, causal or not,
 sliding windows, softcap, P rules R1 and R2, head dims 64/128/256, V as E4M3, E3M2 bytes or
 block-packed E3M2.  Every case runs mxfa_prefill_ws, mxfa_prefill and -- for single-query
-cases -- mxfa_decode, each against the oracle at the north_star tolerance."""
+cases -- mxfa_decode, each against the oracle at the north_star tolerance (a prefill element
+past max-abs must be a traced P code boundary tie, as in test_gpu_attention)."""
 import numpy as np
 import pytest
 
@@ -11,7 +12,7 @@ torch = pytest.importorskip("torch")
 
 import mxfa  # noqa: E402
 import oracle as O  # noqa: E402
-from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, np_, oracle_params  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, explain_max_abs, np_, oracle_params  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +40,7 @@ def _case(i):
                 window=window, softcap=softcap, p_rule=p_rule, v_fmt=v_fmt, seed=9000 + i)
 
 
-@pytest.mark.parametrize("i", range(36))
+@pytest.mark.parametrize("i", list(range(36)) + [286, 292, 812])
 def test_sweep(i):
     c = _case(i)
     print(f"sweep case {i}: {c}", flush=True)
@@ -78,4 +79,18 @@ def test_sweep(i):
         assert np.all(np.isfinite(o)), name
         rel, mab = errors(o, want)
         print(f"   {name}: rel-L2 {rel:.3e} max-abs {mab:.3e}", flush=True)
-        assert rel <= REL_L2_TOL and mab <= MAX_ABS_TOL, name
+        assert rel <= REL_L2_TOL, name
+        if mab > MAX_ABS_TOL:
+            # only P code boundary ties between the kernel's fp32 and the oracle's double P may
+            # exceed the bound (seeds 286, 292 and 812 of this generator do): traced on dense copies
+            # of the first Sk keys, whose O is the strided call's bit for bit
+            assert name != "decode", name
+            pd = mxfa.make_params(B, Hq, Hkv, Sq, Sk, D, v_fmt=c["v_fmt"], **kw)
+            nblk = Sk // 32
+            dev = dict(q=q, qs=qs, k=k[:, :, :Sk].contiguous(), ks=ks[:, :, :Sk].contiguous(),
+                       v=(v[:, :, :nblk] if c["v_fmt"] == mxfa.FMT_E3M2_BLK else v[:, :, :Sk]).contiguous(),
+                       vs=vs[:, :, :nblk].contiguous())
+            od = mxfa.prefill(pd, *(dev[n] for n in ("q", "qs", "k", "ks", "v", "vs")), workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(od, out), "strided and dense calls differ"
+            explain_max_abs(pd, dev, {n: np_(x) for n, x in dev.items()}, o, want)
