@@ -48,6 +48,24 @@ def errors(got, want):
     return rel, mab
 
 
+def sweep_seeds(default, env="MXFA_SWEEP_SEEDS"):
+    """The seeds of a seeded sweep: `default`, or those the environment variable lists
+    ("a-b" for a..b-1, comma-separated items), so that a longer exploratory run is one
+    pytest command, e.g. MXFA_SWEEP_SEEDS=36-2012."""
+    import os
+    spec = os.environ.get(env)
+    if not spec:
+        return list(default)
+    out = []
+    for item in spec.split(","):
+        if "-" in item:
+            a, b = item.split("-")
+            out += list(range(int(a), int(b)))
+        else:
+            out.append(int(item))
+    return out
+
+
 REL_L2_TOL = 5e-3     # north_star: rel-L2 <= 5e-3
 MAX_ABS_TOL = 2e-2    # north_star: max-abs <= 2e-2
 

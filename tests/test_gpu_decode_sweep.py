@@ -12,7 +12,7 @@ torch = pytest.importorskip("torch")
 
 import mxfa  # noqa: E402
 import oracle as O  # noqa: E402
-from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, np_, oracle_params  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, np_, oracle_params, sweep_seeds  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -36,7 +36,7 @@ def _case(i):
                 softcap=softcap, p_rule=p_rule, v_fmt=FMTS[i % 3], waves=waves, rng=rng)
 
 
-@pytest.mark.parametrize("i", range(60))
+@pytest.mark.parametrize("i", sweep_seeds(range(60)))
 def test_decode_sweep(i, monkeypatch):
     c = _case(i)
     rng = c.pop("rng")

@@ -9,7 +9,7 @@ torch = pytest.importorskip("torch")
 
 import mxfa  # noqa: E402
 import oracle as O  # noqa: E402
-from gpuhelp import DEV, np_  # noqa: E402
+from gpuhelp import DEV, np_, sweep_seeds  # noqa: E402
 from mxdata import rel_l2  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -48,6 +48,26 @@ def run_gemm(M, N, K, seed, a_fmt=mxfa.FMT_E4M3, b_fmt=mxfa.FMT_E4M3, srange=(11
                                    (512, 384, 1024), (272, 528, 320)])
 def test_gemm_matches_oracle(M, N, K):
     run_gemm(M, N, K, seed=M + 3 * N + 7 * K)
+
+
+@pytest.mark.parametrize("i", sweep_seeds(range(12), "MXFA_GEMM_SEEDS"))
+def test_gemm_sweep(i, monkeypatch):
+    """Seeded shapes (M = 16 .. 1,024, N = 16 .. 1,104, K = 64 .. 2,496) with E4M3 or E3M2
+    operands through each kernel path (the default choice -- skinny for M <= 128, else the
+    LDS-DMA kernel for E4M3 with K % 128 == 0 -- MXFA_GEMM=big or =reg); MXFA_GEMM_SEEDS=0-300
+    runs the exploratory length."""
+    rng = np.random.default_rng(31000 + i)
+    M = 16 * int(rng.choice([1, 2, 3, 4, 5, 7, 8, 9, 16, 17, 33, 64]))
+    N = 16 * int(rng.integers(1, 70))
+    K = 64 * int(rng.integers(1, 40))
+    af = int(rng.choice([mxfa.FMT_E4M3, mxfa.FMT_E4M3, mxfa.FMT_E3M2]))
+    bf = int(rng.choice([mxfa.FMT_E4M3, mxfa.FMT_E4M3, mxfa.FMT_E3M2]))
+    mode = str(rng.choice(["", "big", "reg"]))
+    if mode:
+        monkeypatch.setenv("MXFA_GEMM", mode)
+    else:
+        monkeypatch.delenv("MXFA_GEMM", raising=False)
+    run_gemm(M, N, K, seed=31000 + i, a_fmt=af, b_fmt=bf)
 
 
 def test_gemm_e3m2_operands_and_wide_scales():

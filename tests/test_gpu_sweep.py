@@ -12,7 +12,7 @@ torch = pytest.importorskip("torch")
 
 import mxfa  # noqa: E402
 import oracle as O  # noqa: E402
-from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, explain_max_abs, np_, oracle_params  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, explain_max_abs, np_, oracle_params, sweep_seeds  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -40,7 +40,7 @@ def _case(i):
                 window=window, softcap=softcap, p_rule=p_rule, v_fmt=v_fmt, seed=9000 + i)
 
 
-@pytest.mark.parametrize("i", list(range(36)) + [286, 292, 812])
+@pytest.mark.parametrize("i", sweep_seeds(list(range(36)) + [286, 292, 812]))
 def test_sweep(i):
     c = _case(i)
     print(f"sweep case {i}: {c}", flush=True)
