@@ -9,7 +9,7 @@ torch = pytest.importorskip("torch")
 
 import mxfa  # noqa: E402
 import oracle as O  # noqa: E402
-from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, np_, oracle_params  # noqa: E402
+from gpuhelp import DEV, MAX_ABS_TOL, REL_L2_TOL, errors, np_, oracle_params, sweep_seeds  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +53,46 @@ def test_append_matches_one_shot_quantization(D, fmt):
         if m < L:                                                     # nothing past the block is written
             assert np.all(np_(cache.k)[:, :, m:] == sentinel)
             assert np.all(np_(cache.v)[:, :, m32:] == sentinel)
+
+
+@pytest.mark.parametrize("i", sweep_seeds(range(6), "MXFA_KV_SEEDS"))
+def test_append_sweep(i):
+    """Seeded random append sequences (chunks of 1-100 tokens, the cache filled to a random
+    length) for D 64/128/256 and V as E4M3, E3M2 bytes or block-packed E3M2: after every
+    append the cache equals the oracle's one-shot quantization of everything so far, and
+    nothing past the open block is written.  MXFA_KV_SEEDS=0-200 runs it longer."""
+    rng = np.random.default_rng(52000 + i)
+    D = int(rng.choice([64, 128, 256]))
+    fmt = (mxfa.FMT_E4M3, mxfa.FMT_E3M2, mxfa.FMT_E3M2_BLK)[i % 3]
+    B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+    L = 32 * int(rng.integers(2, 24))
+    Kf = (rng.standard_normal((B, H, L, D)) * 2.0 ** rng.integers(-8, 8, (1, 1, L, 1))).astype(np.float32)
+    Vf = (rng.standard_normal((B, H, L, D)) * 2.0 ** rng.integers(-8, 8, (1, 1, L, 1))).astype(np.float32)
+    cache = mxfa.KvCache(B, H, D, L, v_fmt=fmt)
+    sentinel = 0x5A
+    for t_ in (cache.k, cache.ks, cache.v, cache.vs):
+        t_.fill_(sentinel)
+    Kd, Vd = torch.from_numpy(Kf).to(DEV), torch.from_numpy(Vf).to(DEV)
+    target = int(rng.integers(1, L + 1))
+    print(f"append sweep {i}: B{B} H{H} D{D} L{L} fmt {fmt} to {target}", flush=True)
+    while cache.length < target:
+        p0 = cache.length
+        n = min(int(rng.integers(1, 101)), target - p0)
+        cache.append(Kd[:, :, p0:p0 + n].contiguous(), Vd[:, :, p0:p0 + n].contiguous())
+        torch.cuda.synchronize()
+        m = cache.length
+        nb = -(-m // 32)
+        kc, ks, vc, vs = expected_cache(Kf, Vf, m, mxfa.FMT_E4M3 if fmt == mxfa.FMT_E4M3 else mxfa.FMT_E3M2)
+        np.testing.assert_array_equal(np_(cache.k)[:, :, :m], kc)
+        np.testing.assert_array_equal(np_(cache.ks)[:, :, :m], ks)
+        if fmt == mxfa.FMT_E3M2_BLK:
+            np.testing.assert_array_equal(np_(cache.v)[:, :, :nb], mxfa.e3m2_to_blk(vc))
+            assert np.all(np_(cache.v)[:, :, nb:] == sentinel)
+        else:
+            np.testing.assert_array_equal(np_(cache.v)[:, :, :32 * nb], vc)
+            assert np.all(np_(cache.v)[:, :, 32 * nb:] == sentinel)
+        np.testing.assert_array_equal(np_(cache.vs)[:, :, :nb], vs)
+        assert np.all(np_(cache.k)[:, :, m:] == sentinel)
 
 
 def test_decode_over_appended_cache():
