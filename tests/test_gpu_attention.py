@@ -189,6 +189,15 @@ def test_decode_ragged_and_e3m2():
     run_decode(2, 16, 8, 2080, 256, seed=32, softcap=30.0)
 
 
+def test_long_context_decode_and_prefill():
+    """Long caches: decode over 262,144 keys (hundreds of key blocks per partial, the split
+    plan at its widest), and a 64-query chunk prefilled at the end of a 131,072-key cache (few
+    work items, 2,048 key blocks each) at D = 256 with softcap and E3M2 V."""
+    run_decode(1, 8, 1, 262144, 128, seed=36)
+    run_case(1, 4, 2, 64, 131072, 256, causal=True, q_pos0=131072 - 64, softcap=30.0, v_fmt=mxfa.FMT_E3M2,
+             seed=37, check_codes=False)
+
+
 def test_decode_config5_all_heads():
     """B=64, Hq=32, Hkv=8, D=128, KV length 8192."""
     p, dev, out = run_decode(64, 32, 8, 8192, 128, seed=33)
