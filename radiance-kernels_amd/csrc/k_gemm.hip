@@ -507,26 +507,54 @@ __device__ __forceinline__ void gemm_dma_impl(const GemmArgs& g) {
     if (kt + 1 < nk) step(std::integral_constant<int, 1>{}, kt + 1);
   }
 
+  // C through LDS: after the last step every stage is free.  Each wave stages PR rows of its
+  // 128 x 32 TJ tile at a time in its own REG bytes ([PR][32 TJ] elements, row-major) and
+  // stores them as 16-byte pieces, 64 lanes covering 1 KB of consecutive rows -- whole
+  // 128-byte lines -- per instruction instead of one element per lane (columns >= N are not
+  // stored: N % 16 == 0 keeps every piece on one side; rows >= M are past the resource).
   const int r = lane & 31, h = lane >> 5;
   const int rows = min(TM, g.M - m0);
-  const int ES = g.c_bf16 ? 2 : 4;
-  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(g.c + (int64_t)m0 * g.N * ES), 0, (int)(uint32_t)((int64_t)rows * g.N * ES), 0x00020000);
+  __syncthreads();
+  constexpr int REG = 4 * TM * TK / NW;   // the four 32 KB A and B stages, split between the waves
+  uint8_t* const reg = (wave < NW / 4 ? sA0 : wave < NW / 2 ? sA1 : wave < 3 * NW / 4 ? sB0 : sB1) +
+                       (wave % (NW / 4)) * REG;
+  auto epilogue = [&](auto es_c) {
+    constexpr int ES = decltype(es_c)::value;
+    constexpr int W = 32 * TJ * ES;       // bytes of one staged row
+    constexpr int PR = REG / W;           // rows per pass
+    constexpr int RPI = 1024 / W;         // rows per store instruction
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.c + (int64_t)m0 * g.N * ES), 0, (int)(uint32_t)((int64_t)rows * g.N * ES), 0x00020000);
 #pragma unroll
-  for (int j = 0; j < TJ; j++) {
-    const int n = n0 + 32 * TJ * wc + 32 * j + r;
-    const uint32_t cb = n < g.N ? (uint32_t)((128 * wr + 4 * h) * g.N + n) * (uint32_t)ES : 0xfffffff0u;
+    for (int p0 = 0; p0 < 128; p0 += PR) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++) {
+        if (32 * i < p0 || 32 * i >= p0 + PR) continue;
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const uint32_t off = n < g.N ? cb + (uint32_t)((32 * i + 8 * (v >> 2) + (v & 3)) * g.N) * (uint32_t)ES : cb;
-        if (g.c_bf16)
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)acc[i][j][v]), rc, off, 0, 0);
-        else
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), rc, off, 0, 0);
+        for (int j = 0; j < TJ; j++)
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            uint8_t* const e = reg + (32 * i - p0 + 8 * (v >> 2) + 4 * h + (v & 3)) * W + (32 * j + r) * ES;
+            if constexpr (ES == 4)
+              *reinterpret_cast<float*>(e) = acc[i][j][v];
+            else
+              *reinterpret_cast<__bf16*>(e) = (__bf16)acc[i][j][v];
+          }
       }
-  }
+#pragma unroll
+      for (int u = 0; u < PR / RPI; u++) {
+        const int lr = u * RPI + lane / (W / 16), ch = lane % (W / 16);
+        const v4i x = *reinterpret_cast<const v4i*>(reg + lr * W + ch * 16);
+        const int col = n0 + 32 * TJ * wc + ch * (16 / ES);
+        const uint32_t off = col < g.N ? (uint32_t)((128 * wr + p0 + lr) * g.N + col) * (uint32_t)ES : 0xfffffff0u;
+        __builtin_amdgcn_raw_buffer_store_b128(x, rc, off, 0, 0);
+      }
+    }
+  };
+  if (g.c_bf16)
+    epilogue(std::integral_constant<int, 2>{});
+  else
+    epilogue(std::integral_constant<int, 4>{});
 }
 
 #ifndef MXFA_GEMM_DMA_WAVES
