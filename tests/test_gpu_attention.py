@@ -198,6 +198,16 @@ def test_long_context_decode_and_prefill():
              seed=37, check_codes=False)
 
 
+def test_gqa_groups_not_powers_of_two():
+    """Query heads per KV head of 3, 6, 7 and 24: the workgroup's heads-per-wave split falls
+    back to the largest power of two dividing the group (1, 2, 1, 8)."""
+    run_case(1, 9, 3, 96, 160, 128, causal=True, q_pos0=64, seed=38)
+    run_case(2, 12, 2, 70, 96, 64, softcap=30.0, seed=39, v_fmt=mxfa.FMT_E3M2)
+    run_case(1, 7, 1, 130, 256, 256, causal=True, q_pos0=126, window=100, seed=40)
+    run_decode(2, 24, 1, 800, 128, seed=41)
+    run_decode(3, 21, 3, 480, 64, seed=42, v_fmt=mxfa.FMT_E3M2)
+
+
 def test_decode_config5_all_heads():
     """B=64, Hq=32, Hkv=8, D=128, KV length 8192."""
     p, dev, out = run_decode(64, 32, 8, 8192, 128, seed=33)
