@@ -275,7 +275,7 @@ static double score_of(const orc_attn_params *p, const double *qd, const double 
  * -inf where masked) and the P code, per 32-key group the P scale code, per block the running
  * (m, l) after it.  NULL members are not written. */
 typedef struct {
-  float *S;
+  double *S;
   uint8_t *codes, *scales;
   double *ml;
 } orc_trace_t;
@@ -307,7 +307,7 @@ static void flash_pass_tr(const orc_attn_params *p, const double *qd, const doub
     }
     double m_new = m > bmax ? m : bmax;
     if (tr && tr->S)
-      for (int t = 0; t < n; t++) tr->S[b0 + t] = (float)S[t];
+      for (int t = 0; t < n; t++) tr->S[b0 + t] = S[t];
     if (m_new == -INFINITY) {                       /* nothing visible yet */
       if (tr && tr->ml) { tr->ml[2 * (b0 / block_n)] = -INFINITY; tr->ml[2 * (b0 / block_n) + 1] = 0.0; }
       if (tr && tr->codes)
@@ -495,7 +495,7 @@ int orc_attention(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_s
  * Returns 0, or -1 on invalid arguments. */
 int orc_attention_trace(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,
                         const uint8_t *k, const uint8_t *k_sc, const uint8_t *v, const uint8_t *v_sc,
-                        int block_n, int64_t bh, int64_t qi, float *S_out, uint8_t *codes_out,
+                        int block_n, int64_t bh, int64_t qi, double *S_out, uint8_t *codes_out,
                         uint8_t *scales_out, double *ml_out) {
   if (!p || p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0 || p->seq_q <= 0 ||
       p->seq_k <= 0 || p->head_dim <= 0 || p->head_dim % 32 || p->seq_k % 32 ||

@@ -108,12 +108,13 @@ int orc_attention(const orc_attn_params *p,
                   const int32_t *heads, int nheads, int nthreads);
 
 /* The stages of query row qi of head bh in a single streaming pass over key blocks of block_n:
- * S_out [seq_k] (scores in natural units after scale, softcap and mask; -inf where masked),
+ * S_out [seq_k] (scores in natural units after scale, softcap and mask, in the double the
+ * recurrence uses; -inf where masked),
  * codes_out [seq_k] (P codes), scales_out [seq_k / 32] (P scale codes), ml_out
  * [ceil(seq_k / block_n)][2] (running max and sum after each block).  Returns 0 or -1. */
 int orc_attention_trace(const orc_attn_params *p, const uint8_t *q, const uint8_t *q_sc,
                         const uint8_t *k, const uint8_t *k_sc, const uint8_t *v, const uint8_t *v_sc,
-                        int block_n, int64_t bh, int64_t qi, float *S_out, uint8_t *codes_out,
+                        int block_n, int64_t bh, int64_t qi, double *S_out, uint8_t *codes_out,
                         uint8_t *scales_out, double *ml_out);
 
 /* Unquantized fp64 softmax attention on the dequantized operands (no P

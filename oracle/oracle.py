@@ -63,7 +63,7 @@ def lib():
                                     ctypes.c_int]
         L.orc_attention.restype = ctypes.c_int
         L.orc_attention_trace.argtypes = [P(AttnParams), u8p, u8p, u8p, u8p, u8p, u8p, ctypes.c_int, ctypes.c_int64,
-                                          ctypes.c_int64, f32p, u8p, u8p, ctypes.c_void_p]
+                                          ctypes.c_int64, ctypes.c_void_p, u8p, u8p, ctypes.c_void_p]
         L.orc_attention_trace.restype = ctypes.c_int
         L.orc_attention_dense.argtypes = [P(AttnParams), u8p, u8p, u8p, u8p, u8p, u8p, f32p,
                                           P(ctypes.c_int32), ctypes.c_int, ctypes.c_int]
@@ -219,15 +219,15 @@ def attention(p, q, qs, k, ks, v, vs, block_n, split_len=0, heads=None, nthreads
 
 def attention_trace(p, q, qs, k, ks, v, vs, block_n, bh, qi):
     """Stages of one query row's streaming pass (orc_attention_trace): dict with S [Sk] (natural
-    units, -inf masked), codes [Sk], scales [Sk/32], m and l [n_blocks] after each block."""
+    units, double, -inf masked), codes [Sk], scales [Sk/32], m and l [n_blocks] after each block."""
     arrs = [np.ascontiguousarray(a, dtype=np.uint8) for a in (q, qs, k, ks, v, vs)]
     Sk = p.seq_k
     nblk = (Sk + block_n - 1) // block_n
-    S = np.full(Sk, np.nan, np.float32)
+    S = np.full(Sk, np.nan, np.float64)
     codes = np.zeros(Sk, np.uint8)
     scales = np.zeros(Sk // 32, np.uint8)
     ml = np.zeros((nblk, 2), np.float64)
-    rc = lib().orc_attention_trace(ctypes.byref(p), *[_u8(a) for a in arrs], block_n, bh, qi, _f32(S), _u8(codes),
+    rc = lib().orc_attention_trace(ctypes.byref(p), *[_u8(a) for a in arrs], block_n, bh, qi, S.ctypes.data_as(ctypes.c_void_p), _u8(codes),
                                    _u8(scales), ml.ctypes.data_as(ctypes.c_void_p))
     if rc != 0:
         raise ValueError("orc_attention_trace rejected its arguments")

@@ -40,7 +40,7 @@ def _case(i):
                 window=window, softcap=softcap, p_rule=p_rule, v_fmt=v_fmt, seed=9000 + i)
 
 
-@pytest.mark.parametrize("i", sweep_seeds(list(range(36)) + [286, 292, 812]))
+@pytest.mark.parametrize("i", sweep_seeds(list(range(36)) + [286, 292, 812, 2286]))
 def test_sweep(i):
     c = _case(i)
     print(f"sweep case {i}: {c}", flush=True)
@@ -82,7 +82,7 @@ def test_sweep(i):
         assert rel <= REL_L2_TOL, name
         if mab > MAX_ABS_TOL:
             # only P code boundary ties between the kernel's fp32 and the oracle's double P may
-            # exceed the bound (seeds 286, 292 and 812 of this generator do): traced on dense copies
+            # exceed the bound (seeds 286, 292, 812 and 2286 of this generator do): traced on dense copies
             # of the first Sk keys, whose O is the strided call's bit for bit
             assert name != "decode", name
             pd = mxfa.make_params(B, Hq, Hkv, Sq, Sk, D, v_fmt=c["v_fmt"], **kw)

@@ -42,7 +42,7 @@ def test_trace_matches_block_recurrence(softcap, p_rule, causal, window, q_pos0)
             S = softcap * np.tanh(S / softcap)
         vis = _visible(np.arange(Sk), q_pos0 + qi, Sk, causal, window)
         S = np.where(vis, S, -np.inf)
-        np.testing.assert_allclose(tr["S"], S.astype(np.float32), rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(tr["S"], S, rtol=1e-10, atol=1e-10)
         m, l = -np.inf, 0.0
         for j in range((Sk + bn - 1) // bn):
             blk = S[j * bn:(j + 1) * bn]
