@@ -207,6 +207,8 @@ def measured_mfma_busy():
 # v_mfma_scale_f32_32x32x64_f8f6f4 (64 clocks each); 1,024 SIMDs at the 2.4 GHz clock the
 # 5.0 PFLOP/s MXFP8 peak is quoted at.
 PEAK_CLOCK_HZ = 2.4e9
+# the shader clock the c3 prefill holds under load: its SQ_BUSY_CYCLES over its launch time
+LOADED_CLOCK_HZ = 2.0e9
 SIMDS = 1024
 
 
@@ -572,7 +574,9 @@ def main():
     result["roofline"]["mfma_ceiling_basis"] = (
         f"{clocks / 1e6:.1f} M SIMD-clocks of MFMA per step ({prefill3_wave_blocks(mxfa, p)} wave-blocks x "
         f"{(p.head_dim // 16) * 64 + (p.head_dim // 32) * 64} clocks: bf16 QK^T + MXFP8 PV) over {SIMDS} SIMDs at "
-        f"{PEAK_CLOCK_HZ / 1e9:.1f} GHz; 0.5 of peak needs the MFMA pipes {50.0 / ceil:.0f}% busy")
+        f"{PEAK_CLOCK_HZ / 1e9:.1f} GHz; 0.5 of peak needs the MFMA pipes {50.0 / ceil:.0f}% busy at that clock, "
+        f"{50.0 / ceil * PEAK_CLOCK_HZ / LOADED_CLOCK_HZ:.0f}% at the ~{LOADED_CLOCK_HZ / 1e9:.1f} GHz the shader clock "
+        f"holds under this load (SQ_BUSY_CYCLES over the launch time)")
 
     # the same workload with the reference device kernels' P rule (R2 compatibility mode)
     p2 = mxfa.make_params(p.batch, p.num_q_heads, p.num_kv_heads, p.seq_q, p.seq_k, p.head_dim, causal=True,
